@@ -1,0 +1,321 @@
+#!/usr/bin/env python3
+"""Benchmark of the routed-expert MoE hot path on one MI355X.
+
+Workload (a "step"): one full MoE layer at decode, M=1 token, D=4096, I=2048:
+router (bf16 gate [256, 4096] + fp32 bias, sqrt(softplus), top-6) -> 6 routed
+FP4 experts (packed e2m1 + E8M0 per 32) -> + one FP8 e4m3 shared expert, with
+synthetic seeded weights generated on the device.  Steps rotate over
+--layers distinct layers (each with its own 256 experts, router and input
+token), so consecutive reuses of the same weights are >= 860 MB apart and
+the 256 MB Infinity Cache cannot serve them.  The step sequence is captured
+in a HIP graph; the timed region replays it.
+
+metric/value: routed-expert bytes (6 x 13,369,344 B) / step time, GB/s.
+roofline: the dominant kernel (stage 1: gate/up of the routed + shared
+experts) -- algorithmic bytes per launch / its average duration, timed live
+with HIP events over a graph of back-to-back launches.
+cpu_baseline: the CPU oracle (a restatement of the reference's PyTorch path:
+per-call FP4/FP8 dequant + fp32 FFN + router) on one thread, on a bounded
+sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import __graft_entry__  # noqa: E402
+
+D, I, E, K = 4096, 2048, 256, 6
+EXPERT_BYTES = 3 * I * D // 2 + 3 * I * D // 32          # 13,369,344
+GATE_UP_BYTES = 2 * (I * D // 2 + I * D // 32)            # w1 + w3 + scales of one routed expert
+DOWN_BYTES = D * I // 2 + D * I // 32                      # w2 + scales
+SHARED_GATE_UP = 2 * I * D + 2 * (I // 128) * (D // 128) * 4
+SHARED_DOWN = D * I + (D // 128) * (I // 128) * 4
+ROUTER_BYTES = E * D * 2 + E * 4
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--layers", type=int, default=8, help="distinct layers rotated through (MALL defeat)")
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-extras", action="store_true", help="skip the M=3 and lm_head side measurements")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(expert-parallel sharding is described in DESIGN.md, not run). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    __graft_entry__.package()
+    from home_seek_amd import expert_store, ops, synthetic
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L = args.layers
+    store = expert_store.HbmExpertStore(L, E, D, I, dev, with_shared=True)
+    store.fill_synthetic(args.seed)
+    routers = [synthetic.router_weights(args.seed, l, E, D, dev) for l in range(L)]
+    xs = [synthetic.hidden(args.seed, 1000 + l, 1, D, dev) for l in range(L)]
+    tables = [store.table(l) for l in range(L)]
+    shareds = [store.shared_entry(l) for l in range(L)]
+    idx_buf = [torch.empty(1, K, dtype=torch.int64, device=dev) for _ in range(L)]
+    w_buf = [torch.empty(1, K, dtype=torch.float32, device=dev) for _ in range(L)]
+    outs = [torch.empty(1, D, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    torch.cuda.synchronize()
+
+    def step(l):
+        idx, w = ops.router_topk(xs[l], routers[l][0], routers[l][1], K, 1.5, out=(idx_buf[l], w_buf[l]))
+        ops.moe_decode(xs[l], idx, w, tables[l], ops.SCALE_E8M0, shareds[l], 10.0, out_bf16=outs[l], d=D, i=I)
+
+    # warm-up (creates workspaces), then capture one rotation
+    for j in range(max(1, args.warmup)):
+        step(j % L)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for l in range(L):
+            step(l)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for l in range(L):
+                step(l)
+    replays = max(1, (args.steps + L - 1) // L)
+    steps = replays * L
+    for _ in range(max(1, args.warmup // L)):
+        graph.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(replays):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = ev0.elapsed_time(ev1) / steps
+    routed_gbs = K * EXPERT_BYTES / (ms_step * 1e-3) / 1e9
+    layer_bytes = K * EXPERT_BYTES + SHARED_GATE_UP + SHARED_DOWN + ROUTER_BYTES
+
+    # ---- dominant kernel: stage 1 (gate/up) alone, back-to-back in a graph
+    def stage_graph(stage):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            for l in range(L):
+                ops.moe_decode_stage(stage, xs[l], idx_buf[l], w_buf[l], tables[l], ops.SCALE_E8M0, shareds[l], 10.0,
+                                     D, I, out_bf16=outs[l])
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=stream):
+                for l in range(L):
+                    ops.moe_decode_stage(stage, xs[l], idx_buf[l], w_buf[l], tables[l], ops.SCALE_E8M0, shareds[l],
+                                         10.0, D, I, out_bf16=outs[l])
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        with torch.cuda.stream(stream):
+            for _ in range(replays):
+                g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (replays * L) * 1e3  # us per launch
+
+    us_stage1 = stage_graph(1)
+    us_stage2 = stage_graph(2)
+    stage1_bytes = K * GATE_UP_BYTES + SHARED_GATE_UP + D * 2 + (K + 1) * 2 * I * 2
+    stage2_bytes = K * DOWN_BYTES + SHARED_DOWN + (K + 1) * 2 * I * 2 + D * 6
+    ach1 = stage1_bytes / (us_stage1 * 1e-6) / 1e9
+    ach2 = stage2_bytes / (us_stage2 * 1e-6) / 1e9
+
+    extras = {}
+    if not args.no_extras:
+        extras = side_measurements(torch, ops, synthetic, store, routers, tables, shareds, stream, args, L)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(args)
+
+    line = {
+        "metric": "MoE layer FP4 expert GB/s (% HBM peak) at M=1/M=3; MTP-verify decode tok/s",
+        "value": round(routed_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp4-e2m1 weights, bf16 MFMA, fp32 accumulate",
+        "data": "synthetic (seeded on device)",
+        "config": {
+            "workload": "one MoE layer at decode M=1: router top-6 of 256 + 6 FP4 experts + FP8 shared expert, "
+                        "D=4096 I=2048",
+            "global_batch": 1,
+            "seq_len": 1,
+            "parallelism": "none (1 GPU)",
+            "layers_rotated": L,
+        },
+        "pct_hbm_peak": round(100.0 * routed_gbs / HBM_PEAK_GBS, 2),
+        "full_layer_gbs": round(layer_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "wall_s_timed": round(wall, 3),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "moe_gate_up_kernel (stage 1)",
+            "achieved": round(ach1, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(ach1 / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": stage1_bytes,
+            "avg_launch_us": round(us_stage1, 3),
+            "stage2": {"kernel": "moe_down_kernel", "achieved": round(ach2, 1), "avg_launch_us": round(us_stage2, 3),
+                       "algorithmic_bytes_per_launch": stage2_bytes},
+        },
+        "cpu_baseline": cpu,
+    }
+    line.update(extras)
+    print(json.dumps(line))
+
+
+def side_measurements(torch, ops, synthetic, store, routers, tables, shareds, stream, args, L):
+    """M=3 verify layer (per-token distinct routing) and the T=3 lm_head + acceptance kernel."""
+    xs3 = [synthetic.hidden(args.seed, 2000 + l, 3, D, store.device) for l in range(L)]
+    uniq = []
+    for l in range(L):
+        idx, _ = ops.router_topk(xs3[l], routers[l][0], routers[l][1], K, 1.5)
+        uniq.append(len(set(idx.reshape(-1).tolist())))
+    outs = [torch.empty(3, D, dtype=torch.bfloat16, device=store.device) for _ in range(L)]
+
+    def step3(l):
+        idx, w = ops.router_topk(xs3[l], routers[l][0], routers[l][1], K, 1.5)
+        ops.moe_decode(xs3[l], idx, w, tables[l], ops.SCALE_E8M0, shareds[l], 10.0, out_bf16=outs[l], d=D, i=I)
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        for l in range(L):
+            step3(l)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            for l in range(L):
+                step3(l)
+    reps = max(2, args.steps // (4 * L))
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    with torch.cuda.stream(stream):
+        for _ in range(reps):
+            g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms3 = e0.elapsed_time(e1) / (reps * L)
+    m3_gbs = (sum(uniq) / L) * EXPERT_BYTES / (ms3 * 1e-3) / 1e9
+
+    vocab = 129280
+    lm = synthetic.normal_bf16(args.seed, synthetic.tag(synthetic.KIND_LM_HEAD), (vocab, D), 0.0, 0.02, store.device)
+    h = synthetic.hidden(args.seed, 3000, 3, D, store.device)
+    ids = torch.tensor([1, 2, 3], device=store.device)
+    gl = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        ops.lm_head_accept(h, lm, ids)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(gl, stream=stream):
+            ops.lm_head_accept(h, lm, ids)
+    gl.replay()
+    torch.cuda.synchronize()
+    reps_l = 20
+    e0.record(stream)
+    with torch.cuda.stream(stream):
+        for _ in range(reps_l):
+            gl.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_lm = e0.elapsed_time(e1) / reps_l
+    del lm
+    return {
+        "m3_layer": {"ms_per_step": round(ms3, 5), "unique_experts_avg": sum(uniq) / L,
+                     "routed_gbs": round(m3_gbs, 1), "pct_hbm_peak": round(100 * m3_gbs / HBM_PEAK_GBS, 2)},
+        "lm_head_t3_accept": {"ms": round(ms_lm, 4), "gbs": round(vocab * D * 2 / (ms_lm * 1e-3) / 1e9, 1)},
+    }
+
+
+def cpu_baseline(args):
+    """Times the CPU oracle on a bounded sample of the same workload (one thread)."""
+    import numpy as np
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    from oracle import oracle as orc
+
+    seed = args.seed
+    n_layers = min(args.layers, 4)
+    prepared = []
+    for l in range(n_layers):
+        gate = orc.gen_normal_bf16(orc.key(seed, orc.tag(orc.KIND_GATE_W, l)), E * D, 0.0, 0.02).reshape(E, D)
+        bias = orc.gen_normal_f32(orc.key(seed, orc.tag(orc.KIND_GATE_BIAS, l)), E, 0.0, 0.01)
+        x = orc.gen_normal_bf16(orc.key(seed, orc.tag(orc.KIND_HIDDEN, 0, 1000 + l)), D, 0.0, 1.0).reshape(1, D)
+        idx, _ = orc.router(x, gate, bias, K, 1.5)
+        raw = {}
+        for e in idx[0]:
+            ex = {}
+            for sub, (nm, r, c) in enumerate((("w1", I, D), ("w3", I, D), ("w2", D, I))):
+                ex[nm] = orc.gen_bytes(orc.key(seed, orc.tag(orc.KIND_FP4_DATA, l, int(e), sub)), r * c // 2).reshape(r, c // 2)
+                ex[nm + "_scale"] = orc.gen_e8m0(orc.key(seed, orc.tag(orc.KIND_FP4_SCALE, l, int(e), sub)), r * c // 32).reshape(r, c // 32)
+            raw[int(e)] = ex
+        sh = orc.gen_shared_expert(seed, l, D, I)
+        prepared.append((gate, bias, x, raw, sh))
+
+    def one_layer(gate, bias, x, raw, sh):
+        idx, w = orc.router(x, gate, bias, K, 1.5)
+        experts = {}
+        for e, ex in raw.items():
+            experts[e] = {nm + "_bf16": orc.dequant_fp4(ex[nm], ex[nm + "_scale"]) for nm in ("w1", "w3", "w2")}
+        shared = {nm + "_bf16": orc.dequant_fp8(sh[nm], sh[nm + "_scale"]) for nm in ("w1", "w3", "w2")}
+        return orc.moe_layer_fp32(x, idx, w, experts, shared, 10.0)
+
+    ctx = threadpool_limits(limits=1) if threadpool_limits else None
+    if ctx:
+        ctx.__enter__()
+    try:
+        one_layer(*prepared[0])
+        n = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds or n < 2:
+            one_layer(*prepared[n % n_layers])
+            n += 1
+        dt = time.perf_counter() - t0
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    return {
+        "value": round(n * K * EXPERT_BYTES / dt / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{n} MoE layers at M=1 (router + per-call FP4/FP8 dequant + fp32 FFN of 6 routed + 1 shared "
+                  f"expert), {dt:.1f} s on one thread; ms/layer {1e3 * dt / n:.1f}",
+    }
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,172 @@
+// lm_head logits + greedy argmax + longest-prefix draft acceptance.
+//
+// Restates the verify tail of _mtp_verify_batched (engine.py:2480-2497):
+//   logits = bf16(h . lm_head^T); pred[t] = argmax(logits[t]) (first index
+//   on ties, as torch.argmax); accept combined_ids[t+1] while it equals
+//   pred[t]; the bonus row is the first mismatch (or the last row).
+// Each logit is the correctly rounded bf16 of the exact dot product: one lane
+// owns one vocab row and sums it in fp64 (bf16 x bf16 products are exact in
+// fp64); the hidden states are pre-widened to fp64 and read with uniform
+// (scalar) loads, so the per-weight cost is 2 conversions + n_tok fp64 FMAs.
+// The vocab-wide argmax is a 64-bit atomic max on (orderable logit, ~index);
+// the last workgroup to finish evaluates the acceptance rule and clears the
+// counters for the next call.
+#include "hsmoe_common.h"
+#include "hsmoe_internal.h"
+
+namespace hsmoe {
+namespace {
+
+constexpr int kMaxTok = 8;
+constexpr int kWaves = 4;
+constexpr int kRowsPerBlock = 64 * kWaves;
+
+struct Workspace {
+  unsigned long long key[kMaxTok];
+  unsigned int done;
+  unsigned int pad;
+  // followed (256-byte aligned) by double h64[n_tok][d]
+};
+
+inline size_t h64_offset() { return 256; }
+
+__global__ void widen_h_kernel(const uint16_t* __restrict__ h, int64_t n, double* __restrict__ h64) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    h64[i] = (double)bf16_bits_to_f32(h[i]);
+}
+
+// Orderable key of a bf16 logit: larger value -> larger key; NaN above all.
+__device__ __forceinline__ unsigned long long logit_key(uint32_t bits, int64_t v) {
+  uint32_t o = (bits & 0x8000u) ? (~bits & 0xffffu) : (bits | 0x8000u);
+  if ((bits & 0x7fffu) > 0x7f80u) o = 0x1ffffu;  // NaN: torch.argmax returns the first NaN
+  return ((unsigned long long)o << 32) | (unsigned long long)(0xffffffffu - (uint32_t)v);
+}
+
+template <int kTok>
+__global__ void __launch_bounds__(64 * kWaves)
+    lm_head_kernel(const uint16_t* __restrict__ w, const double* __restrict__ h64, int64_t d, int64_t vocab,
+                   const int64_t* __restrict__ ids, uint16_t* __restrict__ logits, int64_t* __restrict__ pred_out,
+                   int64_t* __restrict__ result_out, Workspace* __restrict__ ws) {
+  __shared__ unsigned long long s_key[kWaves][kTok];
+  __shared__ int s_last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t v = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x;
+  const bool on = v < vocab;
+  const uint16_t* wr = w + (on ? v : 0) * d;
+  double acc[kTok];
+#pragma unroll
+  for (int t = 0; t < kTok; ++t) acc[t] = 0.0;
+  for (int64_t k0 = 0; k0 < d; k0 += 64) {
+    uint4 q[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) q[b] = *reinterpret_cast<const uint4*>(wr + k0 + 8 * b);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const uint32_t qq[4] = {q[b].x, q[b].y, q[b].z, q[b].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t bits = (e & 1) ? (qq[e >> 1] & 0xffff0000u) : (qq[e >> 1] << 16);
+        const double wv = (double)__uint_as_float(bits);
+#pragma unroll
+        for (int t = 0; t < kTok; ++t) acc[t] = __fma_rn(h64[t * d + k0 + 8 * b + e], wv, acc[t]);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kTok; ++t) {
+    const uint32_t bits = f64_to_bf16_bits(acc[t]);
+    if (on && logits) logits[t * vocab + v] = (uint16_t)bits;
+    unsigned long long k = on ? logit_key(bits, v) : 0ull;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      unsigned long long o = __shfl_xor(k, off, 64);
+      k = o > k ? o : k;
+    }
+    if (lane == 0) s_key[wave][t] = k;
+  }
+  __syncthreads();
+  if (threadIdx.x < kTok) {
+    unsigned long long k = 0;
+#pragma unroll
+    for (int q = 0; q < kWaves; ++q) k = s_key[q][threadIdx.x] > k ? s_key[q][threadIdx.x] : k;
+    atomicMax(&ws->key[threadIdx.x], k);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    unsigned int prev = atomicAdd(&ws->done, 1u);
+    s_last = prev == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last || threadIdx.x != 0) return;
+  __threadfence();
+  int64_t pred[kTok];
+#pragma unroll
+  for (int t = 0; t < kTok; ++t) {
+    unsigned long long k = atomicExch(&ws->key[t], 0ull);
+    pred[t] = (int64_t)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
+    pred_out[t] = pred[t];
+  }
+  int64_t n_acc = 0;
+  for (int t = 0; t + 1 < kTok; ++t) {
+    if (pred[t] != ids[t + 1]) break;
+    ++n_acc;
+  }
+  result_out[0] = n_acc;
+  result_out[1] = n_acc;
+  atomicExch(&ws->done, 0u);
+}
+
+template <int kTok>
+int launch(const uint16_t* w, const double* h64, int64_t d, int64_t vocab, const int64_t* ids, uint16_t* logits,
+           int64_t* pred, int64_t* result, Workspace* ws, hipStream_t st) {
+  const unsigned nb = (unsigned)((vocab + kRowsPerBlock - 1) / kRowsPerBlock);
+  hipLaunchKernelGGL(lm_head_kernel<kTok>, dim3(nb), dim3(64 * kWaves), 0, st, w, h64, d, vocab, ids, logits, pred,
+                     result, ws);
+  return check_launch("hsmoe_lm_head_accept");
+}
+
+}  // namespace
+}  // namespace hsmoe
+
+using namespace hsmoe;
+
+extern "C" size_t hsmoe_lm_head_workspace_size(int64_t n_tok, int64_t vocab) {
+  (void)vocab;
+  if (n_tok < 1 || n_tok > kMaxTok) return 0;
+  return h64_offset() + (size_t)n_tok * 8 * 8192;  // room for d <= 8192
+}
+
+extern "C" int hsmoe_lm_head_accept(const void* h, const void* lm_head, int64_t n_tok, int64_t d, int64_t vocab,
+                                    const int64_t* ids, void* logits_out, int64_t* pred_out, int64_t* result_out,
+                                    void* workspace, size_t workspace_bytes, hsmoe_stream_t stream) {
+  if (!h || !lm_head || !pred_out || !result_out || vocab < 1 || d < 1)
+    return fail(HSMOE_ERR_ARG, "hsmoe_lm_head_accept: null pointer or bad size");
+  if (n_tok < 1 || n_tok > kMaxTok) return fail(HSMOE_ERR_SHAPE, "hsmoe_lm_head_accept: n_tok must be in [1, 8]");
+  if (n_tok > 1 && !ids) return fail(HSMOE_ERR_ARG, "hsmoe_lm_head_accept: ids required when n_tok > 1");
+  if (d % 512 != 0 || d > 8192 || !aligned(lm_head, 16))
+    return fail(HSMOE_ERR_SHAPE, "hsmoe_lm_head_accept: d must be a multiple of 512 (<= 8192), lm_head 16-byte aligned");
+  if (vocab >= 0xffffffffll) return fail(HSMOE_ERR_SHAPE, "hsmoe_lm_head_accept: vocab too large");
+  if (!workspace || workspace_bytes < hsmoe_lm_head_workspace_size(n_tok, vocab) || !aligned(workspace, 256))
+    return fail(HSMOE_ERR_WORKSPACE, "hsmoe_lm_head_accept: zero-filled 256-byte aligned workspace of %zu bytes needed",
+                hsmoe_lm_head_workspace_size(n_tok, vocab));
+  hipStream_t st = (hipStream_t)stream;
+  Workspace* ws = (Workspace*)workspace;
+  double* h64 = (double*)((char*)workspace + h64_offset());
+  hipLaunchKernelGGL(widen_h_kernel, dim3((unsigned)((n_tok * d + 255) / 256)), dim3(256), 0, st, (const uint16_t*)h,
+                     n_tok * d, h64);
+  int rc = check_launch("hsmoe_lm_head_accept(widen)");
+  if (rc) return rc;
+  const uint16_t* w = (const uint16_t*)lm_head;
+  uint16_t* lg = (uint16_t*)logits_out;
+  switch (n_tok) {
+    case 1: return launch<1>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 2: return launch<2>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 3: return launch<3>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 4: return launch<4>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 5: return launch<5>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 6: return launch<6>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 7: return launch<7>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    default: return launch<8>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+  }
+}

@@ -1,0 +1,192 @@
+"""The MoE slice of HomeSeekInferenceEngine, on the HBM expert store and HIP kernels.
+
+Method names, arguments and return values follow the reference engine
+(src/home_seek/inference_engine/engine.py) so that its _forward_layer, generate
+and MTP loop can call them unchanged:
+  _load_expert_weights / _load_expert_raw / _load_expert_fp4_raw /
+  _load_bf16_deq / _load_expert_deq              engine.py:1084-1335
+  _compute_routing_experts / _compute_hash_experts  engine.py:1018-1031
+  _get_shared_expert                              engine.py:1779-1849
+  _forward_ffn                                    engine.py:1410-1541
+  _mtp_verify_batched                             engine.py:2431-2540
+Attention, mHC, KV caches and sampling stay with the host engine; the hooks
+`_snapshot_verify_state` / `_restore_verify_state` are where a full engine
+saves and trims its attention state around a verify (no-ops here).
+Divergences from the reference, all deliberate:
+  * T > 1 uses the same FP4 kernel as T = 1 (the reference switches to a dense
+    BF16 union GEMM, fused_moe.py:458-551) and reads each layer's own experts
+    (the reference's BF16 cache is keyed by (eid, device) and aliases expert
+    e of the first layer that loaded it, engine.py:1319-1323).
+  * no host synchronisation inside _forward_ffn (the reference calls .tolist()
+    on the routing ids, engine.py:1432-1433); _mtp_verify_batched syncs once.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+from ._lib import SCALE_E8M0
+from .expert_store import HbmExpertStore
+from .fused_moe import FusedMoEFFN, SharedExpertFFN
+from .model_config import MoEConfig
+from .router import compute_expert_affinity_with_bias
+
+
+class HomeSeekMoEEngine:
+    def __init__(self, config: MoEConfig, store: HbmExpertStore, layer_weights: dict[int, dict],
+                 lm_head: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None,
+                 embed: torch.Tensor | None = None):
+        self.config = config
+        self.store = store
+        self.device = store.device
+        self._layer_weights = layer_weights
+        self.lm_head = lm_head
+        self.norm_weight = norm_weight
+        self.embed = embed
+        self._fused_moe = FusedMoEFFN(config.n_routed_experts, config.moe_intermediate_size, config.hidden_size,
+                                      config.swiglu_limit)
+        self._shared_ffn = SharedExpertFFN(config.hidden_size, config.moe_intermediate_size, config.swiglu_limit)
+        self._global_pos = 0
+        self._phase = "decode"
+        self._last_routed_idx = None
+
+    # ------------------------------------------------------------ weights
+    def _get_layer_weights(self, layer_idx: int) -> dict:
+        return self._layer_weights[layer_idx]
+
+    def _load_expert_fp4_raw(self, layer_idx: int, eid: int):
+        """(w1, w1_scale, w3, w3_scale, w2, w2_scale) device views (E8M0 scales), or None."""
+        try:
+            return self.store.expert_views(layer_idx, eid)
+        except IndexError:
+            return None
+
+    def _load_expert_weights(self, layer_idx: int, eid: int):
+        """((w1, s1, fmt), (w3, s3, fmt), (w2, s2, fmt)) with fmt "fp4_gpu" (engine.py:1084-1129)."""
+        raw = self._load_expert_fp4_raw(layer_idx, eid)
+        if raw is None:
+            return None
+        w1, s1, w3, s3, w2, s2 = raw
+        return (w1, s1, "fp4_gpu"), (w3, s3, "fp4_gpu"), (w2, s2, "fp4_gpu")
+
+    _load_expert_raw = _load_expert_weights
+
+    def _load_bf16_deq(self, layer_idx: int, eid: int):
+        """BF16 (w1, w3, w2) of this layer's expert, dequantised on demand (no cross-layer alias)."""
+        raw = self._load_expert_fp4_raw(layer_idx, eid)
+        if raw is None:
+            return None
+        w1, s1, w3, s3, w2, s2 = raw
+        return ops.fp4_dequant_bf16(w1, s1), ops.fp4_dequant_bf16(w3, s3), ops.fp4_dequant_bf16(w2, s2)
+
+    _load_expert_deq = _load_bf16_deq
+
+    def _get_shared_expert(self, layer_idx: int):
+        """BF16 (w1, w3, w2) of the FP8 shared expert (load_fp8_weight, weight_loader.py:22-32)."""
+        views = self.store.shared_views(layer_idx)
+        if views is None:
+            return None
+        w1, s1, w3, s3, w2, s2 = views
+        return ops.fp8_dequant_bf16(w1, s1), ops.fp8_dequant_bf16(w3, s3), ops.fp8_dequant_bf16(w2, s2)
+
+    # ------------------------------------------------------------ routing
+    def _compute_hash_experts(self, input_ids: torch.Tensor, layer_idx: int, tid2eid: torch.Tensor):
+        """engine.py:1018-1023: ids from the token table, weight 1/k each."""
+        B, T = input_ids.shape
+        eids = tid2eid[input_ids]
+        k = self.config.num_experts_per_tok
+        weights = torch.full((B, T, k), 1.0 / k, device=input_ids.device)
+        return eids, weights
+
+    def _compute_routing_experts(self, hidden_states, gate_w, gate_bias):
+        return compute_expert_affinity_with_bias(hidden_states, gate_w, gate_bias,
+                                                 top_k=self.config.num_experts_per_tok,
+                                                 routed_scaling_factor=self.config.routed_scaling_factor)
+
+    # ------------------------------------------------------------ FFN
+    def _forward_ffn(self, hidden_states: torch.Tensor, lw: dict, layer_idx: int, input_ids=None,
+                     out_f32: torch.Tensor | None = None):
+        """Router (or hash routing) + routed FP4 experts + FP8 shared expert -> ([B, T, D], set())."""
+        gate_w = lw.get("ffn.gate.weight")
+        if gate_w is None:
+            return torch.zeros_like(hidden_states), set()
+        gate_bias = lw.get("ffn.gate.bias")
+        tid2eid = lw.get("ffn.gate.tid2eid")
+        B, T, D = hidden_states.shape
+        flat = hidden_states.reshape(B * T, D)
+        if layer_idx < self.config.num_hash_layers and tid2eid is not None and input_ids is not None:
+            idx, w = self._compute_hash_experts(input_ids.to(hidden_states.device), layer_idx, tid2eid)
+        else:
+            idx, w = self._compute_routing_experts(flat, gate_w, gate_bias)
+        k = self.config.num_experts_per_tok
+        idx = idx.reshape(B * T, k)
+        w = w.reshape(B * T, k)
+        self._last_routed_idx = idx
+        out = self._fused_moe.forward_table(flat, idx, w, self.store.table(layer_idx), SCALE_E8M0,
+                                            self.store.shared_entry(layer_idx), out_f32=out_f32)
+        return out.reshape(B, T, D).to(hidden_states.dtype), set()
+
+    # ------------------------------------------------------------ MTP verify
+    def _snapshot_verify_state(self):
+        return None
+
+    def _restore_verify_state(self, snapshot, n_accept: int, t_total: int) -> None:
+        return None
+
+    def _final_hidden(self, h: torch.Tensor) -> torch.Tensor:
+        """h [B, T, D] after the last layer -> normed hidden [B*T, D] (engine.py:2480-2482)."""
+        h2 = h.reshape(-1, h.shape[-1])
+        if self.norm_weight is not None:
+            h2 = rms_norm(h2, self.norm_weight, self.config.rms_norm_eps)
+        return h2
+
+    @torch.no_grad()
+    def _mtp_verify_batched(self, draft_ids, temperature: float = 0.6, main_pred_id=None):
+        """One fused forward of [main_pred, drafts] (engine.py:2431-2540) ->
+        (n_accept, bonus_logits [1, V]); greedy acceptance on the device."""
+        if not isinstance(draft_ids, torch.Tensor) or draft_ids.shape[1] == 0:
+            return 0, None
+        combined = torch.cat([main_pred_id, draft_ids], dim=-1) if main_pred_id is not None else draft_ids
+        t_total = combined.shape[1]
+        snap = self._snapshot_verify_state()
+        pos_bak = self._global_pos
+        n_accept = 0
+        bonus_logits = None
+        try:
+            self._global_pos = pos_bak + 1
+            self._phase = "verify"
+            h = self._embed(combined)
+            for layer_idx in range(self.config.num_hidden_layers):
+                h, _ = self._forward_layer(h, self._get_layer_weights(layer_idx), layer_idx, combined)
+            hf = self._final_hidden(h)
+            logits, pred, result = ops.lm_head_accept(hf, self.lm_head, combined.reshape(-1))
+            n_accept, bonus_row = (int(v) for v in result.tolist())  # the one host sync per verify
+            bonus_logits = logits[bonus_row:bonus_row + 1]
+        finally:
+            self._global_pos = pos_bak + n_accept
+            self._restore_verify_state(snap, n_accept, t_total)
+        return n_accept, bonus_logits
+
+    # ------------------------------------------------------------ layer stand-in
+    def _embed(self, ids: torch.Tensor) -> torch.Tensor:
+        if self.embed is None:
+            raise RuntimeError("no embedding table: pass embed= or override _embed")
+        return self.embed[ids].to(torch.bfloat16)
+
+    def _forward_layer(self, h: torch.Tensor, lw: dict, layer_idx: int, input_ids=None):
+        """Layer with attention replaced by a fixed residual lw["attn.residual"] [D]:
+        h = h + r; h = h + FFN(rms_norm(h, ffn_norm))  (engine.py:2653-2690 without mHC)."""
+        r = lw.get("attn.residual")
+        if r is not None:
+            h = h + r
+        hn = h
+        norm_w = lw.get("ffn_norm.weight")
+        if norm_w is not None:
+            hn = rms_norm(h.reshape(-1, h.shape[-1]), norm_w, self.config.rms_norm_eps).reshape(h.shape)
+        ffn_out, used = self._forward_ffn(hn, lw, layer_idx, input_ids)
+        return h + ffn_out, used
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """utils.py:6-9 on the HIP kernel: fp32 mean of squares, x*rsqrt(var+eps)*w, cast back."""
+    return ops.rms_norm(x, weight, eps)

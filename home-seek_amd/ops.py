@@ -1,0 +1,262 @@
+"""Torch-facing wrappers of the libhsmoe entry points.
+
+Each function takes device tensors, checks shapes on the host, and enqueues
+the HIP kernels on the current torch stream.  Workspaces are zero-filled once
+per (device, stream, purpose) and reused; kernels leave their counters at
+zero, so stream-ordered calls can share them.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import SCALE_E8M0, SCALE_F32, check, lib, ptr, require_cuda, stream_ptr
+
+__all__ = [
+    "SCALE_E8M0", "SCALE_F32", "scale_kind_of", "fp4_dequant_bf16", "fp8_dequant_bf16", "router_topk",
+    "moe_decode", "lm_head_accept", "expert_table", "shared_entry", "MAX_DECODE_TOKENS",
+]
+
+MAX_DECODE_TOKENS = 8
+
+_workspaces: dict[tuple, torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, purpose: str, nbytes: int) -> torch.Tensor:
+    key = (device.index, stream_ptr(device), purpose)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def scale_kind_of(scale: torch.Tensor) -> tuple[int, torch.Tensor]:
+    """E8M0 bytes stay bytes; every other dtype is taken by value as fp32 (as
+    `sf.float()` does in fused_moe.py:25)."""
+    if scale.dtype == torch.float8_e8m0fnu:
+        return SCALE_E8M0, scale.view(torch.uint8)
+    if scale.dtype != torch.float32:
+        scale = scale.to(torch.float32)
+    return SCALE_F32, scale
+
+
+def fp4_dequant_bf16(packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """bf16 [N, K] from packed e2m1 [N, K/2] and per-32-column scales [N, K/32]."""
+    dev = require_cuda(packed, scale)
+    if packed.dtype not in (torch.int8, torch.uint8):
+        raise TypeError(f"packed FP4 must be int8/uint8, got {packed.dtype}")
+    if packed.dim() != 2:
+        raise ValueError("packed FP4 must be 2-D [N, K/2]")
+    n, kh = packed.shape
+    k = kh * 2
+    kind, sc = scale_kind_of(scale)
+    if sc.numel() == 1:
+        sc = sc.reshape(1, 1).expand(n, k // 32)
+    if tuple(sc.shape) != (n, k // 32):
+        raise ValueError(f"scale shape {tuple(scale.shape)} does not match [{n}, {k // 32}]")
+    packed = packed.contiguous()
+    sc = sc.contiguous()
+    out = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
+    rc = lib().hsmoe_fp4_dequant_bf16(ptr(packed), ptr(sc), kind, n, k, kh, k // 32, ptr(out), k, stream_ptr(dev))
+    check(rc, "hsmoe_fp4_dequant_bf16")
+    return out
+
+
+def fp8_dequant_bf16(data: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """bf16 [N, K] from e4m3 [N, K] and fp32 (or E8M0) 128x128 block scales."""
+    dev = require_cuda(data, scale)
+    if data.dtype not in (torch.float8_e4m3fn, torch.uint8, torch.int8):
+        raise TypeError(f"FP8 weight must be float8_e4m3fn, got {data.dtype}")
+    n, k = data.shape
+    if scale.dtype == torch.float8_e8m0fnu or scale.element_size() == 1:
+        # _ue8m0_to_f32 (weight_loader.py:14-19): bits = e << 23
+        scale = (scale.view(torch.uint8).to(torch.int32) << 23).view(torch.float32)
+    scale = scale.to(torch.float32).contiguous()
+    if tuple(scale.shape) != ((n + 127) // 128, (k + 127) // 128):
+        raise ValueError(f"block scale shape {tuple(scale.shape)} does not match {n}x{k} / 128")
+    data = data.contiguous().view(torch.uint8)
+    out = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
+    check(lib().hsmoe_fp8_dequant_bf16(ptr(data), ptr(scale), n, k, ptr(out), stream_ptr(dev)),
+          "hsmoe_fp8_dequant_bf16")
+    return out
+
+
+def router_topk(x: torch.Tensor, gate_w: torch.Tensor, bias: torch.Tensor | None, top_k: int = 6,
+                scaling: float = 1.5, want_logits: bool = False, out: tuple | None = None):
+    """(idx int64 [M, k], w fp32 [M, k][, logits bf16 [M, E]]) -- see hsmoe_router_topk.
+    `out` = (idx, w) preallocated outputs to fill."""
+    dev = require_cuda(x, gate_w, bias)
+    x = x.to(torch.bfloat16).contiguous()
+    gate_w = gate_w.to(torch.bfloat16).contiguous()
+    m, d = x.shape
+    e = gate_w.shape[0]
+    if gate_w.shape[1] != d:
+        raise ValueError(f"gate weight {tuple(gate_w.shape)} does not match hidden size {d}")
+    if bias is not None:
+        bias = bias.to(torch.float32).contiguous()
+    if out is not None:
+        idx, w = out
+        if idx.shape != (m, top_k) or w.shape != (m, top_k) or idx.dtype != torch.int64 or w.dtype != torch.float32:
+            raise ValueError("router_topk out tensors must be int64 / fp32 [M, top_k]")
+    else:
+        idx = torch.empty(m, top_k, dtype=torch.int64, device=dev)
+        w = torch.empty(m, top_k, dtype=torch.float32, device=dev)
+    logits = torch.empty(m, e, dtype=torch.bfloat16, device=dev) if want_logits else None
+    nbytes = lib().hsmoe_router_workspace_size(m, e)
+    ws = _workspace(dev, "router", nbytes)
+    rc = lib().hsmoe_router_topk(ptr(x), ptr(gate_w), ptr(bias), m, d, e, top_k, scaling, ptr(idx), ptr(w),
+                                 ptr(logits), ptr(ws), ws.numel(), stream_ptr(dev))
+    check(rc, "hsmoe_router_topk")
+    return (idx, w, logits) if want_logits else (idx, w)
+
+
+def expert_table(entries: list, device: torch.device) -> torch.Tensor:
+    """uint64 [n][6] device table from per-expert tuples.
+
+    An entry is None (absent expert), a 6-tuple (w1, s1, w3, s3, w2, s2) of FP4
+    tensors, or a 3-tuple (w1, w3, w2) of bf16 tensors."""
+    rows = []
+    for ent in entries:
+        if ent is None:
+            rows.append([0] * 6)
+        elif len(ent) == 6:
+            rows.append([t.data_ptr() for t in ent])
+        elif len(ent) == 3:
+            w1, w3, w2 = ent
+            rows.append([w1.data_ptr(), 0, w3.data_ptr(), 0, w2.data_ptr(), 0])
+        else:
+            raise ValueError(f"expert entry of length {len(ent)}")
+    host = torch.tensor(rows, dtype=torch.int64)
+    return host.to(device, non_blocking=False)
+
+
+def shared_entry(w1, s1, w3, s3, w2, s2, device: torch.device) -> torch.Tensor:
+    """uint64 [6] device entry of the shared expert (e4m3 + fp32 block scales,
+    or bf16 weights with s1 = s3 = s2 = None)."""
+    vals = [t.data_ptr() if t is not None else 0 for t in (w1, s1, w3, s3, w2, s2)]
+    return torch.tensor(vals, dtype=torch.int64).to(device)
+
+
+def moe_decode(x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor, table: torch.Tensor,
+               scale_kind: int, shared: torch.Tensor | None = None, swiglu_limit: float = 10.0,
+               out_bf16: torch.Tensor | None = None, out_f32: torch.Tensor | None = None,
+               d: int | None = None, i: int | None = None):
+    """Routed (+ shared) SwiGLU FFN for M <= 8 tokens; returns (out_bf16, out_f32)."""
+    dev = require_cuda(x, topk_idx, topk_w, table, shared)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"hidden states must be bf16, got {x.dtype}")
+    x = x.contiguous()
+    m, dd = x.shape
+    d = dd if d is None else d
+    if i is None:
+        raise ValueError("intermediate size i is required")
+    if m > MAX_DECODE_TOKENS:
+        raise ValueError(f"moe_decode handles at most {MAX_DECODE_TOKENS} tokens, got {m}")
+    topk_idx = topk_idx.to(torch.int64).contiguous()
+    topk_w = topk_w.to(torch.float32).contiguous()
+    k = topk_idx.shape[1]
+    if out_bf16 is None:
+        out_bf16 = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
+    nbytes = lib().hsmoe_moe_decode_workspace_size(m, d, i, k)
+    ws = _workspace(dev, "decode", nbytes)
+    rc = lib().hsmoe_moe_decode(ptr(x), m, d, i, ptr(topk_idx), ptr(topk_w), k, ptr(table), table.shape[0],
+                                scale_kind, ptr(shared), swiglu_limit, ptr(out_f32), ptr(out_bf16), ptr(ws),
+                                ws.numel(), stream_ptr(dev))
+    check(rc, "hsmoe_moe_decode")
+    return out_bf16, out_f32
+
+
+def moe_decode_stage(stage: int, x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor,
+                     table: torch.Tensor, scale_kind: int, shared: torch.Tensor | None, swiglu_limit: float,
+                     d: int, i: int, out_bf16: torch.Tensor | None = None, out_f32: torch.Tensor | None = None):
+    """Launches stage 1 (gate/up) or stage 2 (down) of moe_decode alone; inputs
+    must already be contiguous bf16 / int64 / fp32 device tensors."""
+    dev = x.device
+    m = x.shape[0]
+    k = topk_idx.shape[1]
+    ws = _workspace(dev, "decode", lib().hsmoe_moe_decode_workspace_size(m, d, i, k))
+    if stage == 1:
+        rc = lib().hsmoe_moe_gate_up(ptr(x), m, d, i, ptr(topk_idx), ptr(topk_w), k, ptr(table), table.shape[0],
+                                     scale_kind, ptr(shared), swiglu_limit, ptr(ws), ws.numel(), stream_ptr(dev))
+    else:
+        rc = lib().hsmoe_moe_down(ptr(x), m, d, i, ptr(topk_idx), ptr(topk_w), k, ptr(table), table.shape[0],
+                                  scale_kind, ptr(shared), ptr(out_f32), ptr(out_bf16), ptr(ws), ws.numel(),
+                                  stream_ptr(dev))
+    check(rc, f"moe_decode stage {stage}")
+
+
+def lm_head_accept(h: torch.Tensor, lm_head: torch.Tensor, ids: torch.Tensor | None = None,
+                   want_logits: bool = True):
+    """(logits bf16 [T, V] | None, pred int64 [T], result int64 [2] = (n_accept, bonus_row))."""
+    dev = require_cuda(h, lm_head, ids)
+    h = h.to(torch.bfloat16).contiguous()
+    n, d = h.shape
+    vocab = lm_head.shape[0]
+    if lm_head.dtype != torch.bfloat16 or not lm_head.is_contiguous():
+        raise TypeError("lm_head must be a contiguous bf16 [V, D] tensor")
+    if ids is not None:
+        ids = ids.reshape(-1).to(torch.int64).contiguous()
+        if ids.numel() != n:
+            raise ValueError("ids must have one entry per hidden row")
+    logits = torch.empty(n, vocab, dtype=torch.bfloat16, device=dev) if want_logits else None
+    pred = torch.empty(n, dtype=torch.int64, device=dev)
+    result = torch.empty(2, dtype=torch.int64, device=dev)
+    nbytes = lib().hsmoe_lm_head_workspace_size(n, vocab)
+    ws = _workspace(dev, "lm_head", nbytes)
+    rc = lib().hsmoe_lm_head_accept(ptr(h), ptr(lm_head), n, d, vocab, ptr(ids), ptr(logits), ptr(pred),
+                                    ptr(result), ptr(ws), ws.numel(), stream_ptr(dev))
+    check(rc, "hsmoe_lm_head_accept")
+    return logits, pred, result
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """bf16 RMSNorm over the last dimension (utils.py:6-9)."""
+    dev = require_cuda(x, weight)
+    if x.dtype != torch.bfloat16:
+        raise TypeError("rms_norm takes bf16 input")
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1]).contiguous()
+    w = weight.to(torch.bfloat16).contiguous()
+    out = torch.empty_like(x2)
+    check(lib().hsmoe_rms_norm(ptr(x2), ptr(w), x2.shape[0], x2.shape[1], eps, ptr(out), stream_ptr(dev)),
+          "hsmoe_rms_norm")
+    return out.reshape(shape)
+
+
+# ---------------------------------------------------------------- generators
+
+def gen_bytes(key: int, out: torch.Tensor, e4m3: bool = False) -> torch.Tensor:
+    dev = require_cuda(out)
+    fn = lib().hsmoe_gen_e4m3 if e4m3 else lib().hsmoe_gen_bytes
+    check(fn(key, out.numel() * out.element_size(), ptr(out), stream_ptr(dev)), "hsmoe_gen_bytes")
+    return out
+
+
+def gen_e8m0(key: int, out: torch.Tensor, lo: int = 119, span: int = 6) -> torch.Tensor:
+    dev = require_cuda(out)
+    check(lib().hsmoe_gen_e8m0(key, out.numel(), lo, span, ptr(out), stream_ptr(dev)), "hsmoe_gen_e8m0")
+    return out
+
+
+def gen_normal(key: int, out: torch.Tensor, mean: float, std: float) -> torch.Tensor:
+    dev = require_cuda(out)
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("gen_normal fills bf16 or fp32 tensors")
+    check(lib().hsmoe_gen_normal(key, out.numel(), mean, std, int(out.dtype == torch.bfloat16), ptr(out),
+                                 stream_ptr(dev)), "hsmoe_gen_normal")
+    return out
+
+
+def gen_uniform(key: int, out: torch.Tensor, lo: float, hi: float, mul: float = 1.0) -> torch.Tensor:
+    dev = require_cuda(out)
+    if out.dtype != torch.float32:
+        raise TypeError("gen_uniform fills fp32 tensors")
+    check(lib().hsmoe_gen_uniform(key, out.numel(), lo, hi, mul, ptr(out), stream_ptr(dev)), "hsmoe_gen_uniform")
+    return out
+
+
+def key(seed: int, tag: int) -> int:
+    """Stream key = splitmix64 output number tag+1 for `seed` (same as the device's rand64)."""
+    from .synthetic import rand64
+    return rand64(seed, tag)

@@ -1,0 +1,181 @@
+/*
+ * libhsmoe -- C ABI of the MI355X (gfx950) routed-expert MoE hot path.
+ *
+ * Conventions
+ *   - Every pointer argument named *_dev is device memory; the library never
+ *     allocates, frees or copies user memory.  Scratch memory comes from a
+ *     caller-provided `workspace` of at least the size the matching
+ *     *_workspace_size() call returns, zero-filled once when it is allocated
+ *     (kernels leave their counters at zero when they finish).
+ *   - bf16 tensors are passed as raw 16-bit storage, row-major, contiguous
+ *     unless a row stride argument says otherwise.
+ *   - All work is enqueued on `stream` (a hipStream_t; NULL is the default
+ *     stream); nothing blocks the host.
+ *   - Return value: HSMOE_OK (0) or a negative HSMOE_ERR_* code; the text of
+ *     the last error of the calling thread is hsmoe_last_error().
+ *   - Calls that share one workspace must not overlap in time.
+ */
+#ifndef HSMOE_H_
+#define HSMOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HSMOE_VERSION 1
+
+#define HSMOE_OK 0
+#define HSMOE_ERR_ARG (-1)        /* null pointer, bad count, bad enum */
+#define HSMOE_ERR_SHAPE (-2)      /* shape/alignment outside what a kernel supports */
+#define HSMOE_ERR_LAUNCH (-3)     /* HIP reported an error at launch */
+#define HSMOE_ERR_WORKSPACE (-4)  /* workspace missing or too small */
+
+/* Scale encodings of FP4 weights (one scale per 32 consecutive columns). */
+#define HSMOE_SCALE_E8M0 0 /* uint8 exponent e: 2^(e-127), e == 255 is NaN */
+#define HSMOE_SCALE_F32 1  /* fp32 value */
+
+typedef void* hsmoe_stream_t; /* a hipStream_t */
+
+int hsmoe_version(void);
+const char* hsmoe_last_error(void);
+void hsmoe_clear_error(void);
+
+/* ---------------------------------------------------------------------------
+ * FP4 (e2m1, two codes per byte, low nibble = even column) -> bf16.
+ *   out[n, c] = bf16(e2m1(code[n, c]) * scale[n, c / 32])
+ * Replaces triton_dequantize_fp4_to_bf16 / _dequantize_fp4_to_bf16
+ * (reference src/home_seek/fused_moe.py:672-710 and fused_moe.py:11-31) and the
+ * dequant of load_fp4_weight (src/home_seek/inference_engine/weight_loader.py:35-45).
+ * k must be a multiple of 32; row strides are in elements of each tensor
+ * (bytes for packed, scale entries, bf16 entries for out) and keep 16-byte
+ * alignment of packed rows.
+ */
+int hsmoe_fp4_dequant_bf16(const void* packed_dev, const void* scale_dev, int scale_kind, int64_t n_rows,
+                           int64_t k, int64_t packed_row_stride, int64_t scale_row_stride, void* out_dev,
+                           int64_t out_row_stride, hsmoe_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * FP8 e4m3fn with one scale per 128x128 block -> bf16.
+ *   out[n, c] = bf16(fp32(e4m3[n, c]) * scale[n / 128, c / 128])
+ * Replaces load_fp8_weight -> cast_back(..., 'bf16', (128, 128))
+ * (reference src/home_seek/inference_engine/weight_loader.py:22-32,
+ * src/home_seek/_fp4.py:98-110).  scale is fp32 [ceil(n/128), ceil(k/128)].
+ */
+int hsmoe_fp8_dequant_bf16(const void* data_dev, const float* scale_dev, int64_t n_rows, int64_t k, void* out_dev,
+                           hsmoe_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Router: sqrt(softplus) scores, stable top-k, renormalised weights.
+ * Replaces compute_expert_affinity_with_bias / compute_expert_affinity
+ * (reference src/home_seek/router.py:10-36) as called by
+ * HomeSeekInferenceEngine._compute_routing_experts (engine.py:1025-1031).
+ *   logit[m, e] = bf16(x[m] . gate_w[e])        (exact sum, one rounding)
+ *   if bias:      logit = bf16(logit + bf16(bias[e]))
+ *   score       = sqrt(softplus(float(logit)))  (softplus threshold 20)
+ *   idx[m, :]   = indices of the top_k scores, ties -> lower index first
+ *   w[m, j]     = score[idx[m, j]] / max(sum_j score[idx[m, j]], 1e-20) * scaling
+ * x: bf16 [m, d]; gate_w: bf16 [n_experts, d]; bias: fp32 [n_experts] or NULL.
+ * idx_out: int64 [m, top_k]; w_out: fp32 [m, top_k]; logits_out: bf16
+ * [m, n_experts] or NULL.  n_experts <= 1024, top_k <= 16, d % 256 == 0.
+ */
+size_t hsmoe_router_workspace_size(int64_t m, int64_t n_experts);
+int hsmoe_router_topk(const void* x_dev, const void* gate_w_dev, const float* bias_dev, int64_t m, int64_t d,
+                      int64_t n_experts, int top_k, float scaling, int64_t* idx_out_dev, float* w_out_dev,
+                      void* logits_out_dev, void* workspace_dev, size_t workspace_bytes, hsmoe_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused routed-expert SwiGLU FFN for m <= 8 tokens (decode, MTP verify).
+ * Replaces FusedMoEFFN.forward / .forward_m1_fp4 and, when `shared` is given,
+ * the SharedExpertFFN add of _forward_ffn (reference src/home_seek/fused_moe.py:447-563,
+ * 573-598, 980-1227; src/home_seek/inference_engine/engine.py:1386-1541).
+ *   for every token t and selected expert e (topk_idx[t, j] = e, 0 <= e < n_experts):
+ *     gate = x[t] . W1e^T, up = x[t] . W3e^T          (fp32 accumulation)
+ *     a    = min(gate, L) * sigmoid(min(gate, L)) * clamp(up, -L, L)
+ *     out[t] += topk_w[t, j] * (a . W2e^T)
+ *   plus, if shared != NULL, the same FFN of the FP8 shared expert with weight 1.
+ * W = bf16(dequant) of the FP4 weights, exactly as hsmoe_fp4_dequant_bf16.
+ * expert_table: device uint64 [n_experts][6] = {w1, w1_scale, w3, w3_scale,
+ * w2, w2_scale} device addresses, w1/w3 packed [i, d/2], w2 packed [d, i/2],
+ * scales [i, d/32] / [d, i/32] of `scale_kind`.  An entry whose w1_scale is 0
+ * holds bf16 weights instead (w1/w3 [i, d], w2 [d, i]: the 3-tuple loaders of
+ * the reference).  A zero w1 address marks an absent expert (skipped, like a
+ * loader returning None).
+ * shared: device uint64 [6] of e4m3 w1 [i, d], w3 [i, d], w2 [d, i] and fp32
+ * block scales [i/128, d/128], [i/128, d/128], [d/128, i/128] (or, with zero
+ * scale addresses, bf16 weights); or NULL.
+ * Ids < 0 or >= n_experts are ignored.  out_f32 (fp32 [m, d], optional) and
+ * out_bf16 (bf16 [m, d], optional) receive the result.
+ * m in [1, 8], d % 512 == 0, i % 512 == 0, top_k <= 16.
+ */
+size_t hsmoe_moe_decode_workspace_size(int64_t m, int64_t d, int64_t i, int top_k);
+int hsmoe_moe_decode(const void* x_dev, int64_t m, int64_t d, int64_t i, const int64_t* topk_idx_dev,
+                     const float* topk_w_dev, int top_k, const uint64_t* expert_table_dev, int64_t n_experts,
+                     int scale_kind, const uint64_t* shared_dev, float swiglu_limit, float* out_f32_dev,
+                     void* out_bf16_dev, void* workspace_dev, size_t workspace_bytes, hsmoe_stream_t stream);
+
+/* The two stages of hsmoe_moe_decode as separate launches (same arguments and
+ * workspace): stage 1 computes the weighted SwiGLU activations of every
+ * selected expert into the workspace, stage 2 the down projection and the
+ * cross-expert sum.  hsmoe_moe_down must follow hsmoe_moe_gate_up on the same
+ * stream with the same inputs and workspace.  Lets a caller place other work
+ * between the stages or time each one; no separate counterpart in the
+ * reference (whose M=1 route also runs a gate/up and a down kernel per expert,
+ * fused_moe.py:980-1144). */
+int hsmoe_moe_gate_up(const void* x_dev, int64_t m, int64_t d, int64_t i, const int64_t* topk_idx_dev,
+                      const float* topk_w_dev, int top_k, const uint64_t* expert_table_dev, int64_t n_experts,
+                      int scale_kind, const uint64_t* shared_dev, float swiglu_limit, void* workspace_dev,
+                      size_t workspace_bytes, hsmoe_stream_t stream);
+int hsmoe_moe_down(const void* x_dev, int64_t m, int64_t d, int64_t i, const int64_t* topk_idx_dev,
+                   const float* topk_w_dev, int top_k, const uint64_t* expert_table_dev, int64_t n_experts,
+                   int scale_kind, const uint64_t* shared_dev, float* out_f32_dev, void* out_bf16_dev,
+                   void* workspace_dev, size_t workspace_bytes, hsmoe_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * lm_head logits + greedy argmax + longest-prefix draft acceptance.
+ * Replaces the logits / acceptance loop of _mtp_verify_batched
+ * (reference src/home_seek/inference_engine/engine.py:2480-2497) and the greedy
+ * decode argmax (engine.py:2846-2853).
+ *   logits[t, v] = bf16(h[t] . lm_head[v])   (exact sum, one rounding)
+ *   pred[t]      = argmax_v logits[t, v]     (first index on ties)
+ *   n_accept     = number of leading t < n_tok-1 with pred[t] == ids[t+1]
+ *   bonus_row    = n_accept (the first mismatch or the last row)
+ * h: bf16 [n_tok, d]; lm_head: bf16 [vocab, d]; ids: int64 [n_tok] (may be
+ * NULL when n_tok == 1); logits_out: bf16 [n_tok, vocab] or NULL;
+ * pred_out: int64 [n_tok]; result_out: int64 [2] = {n_accept, bonus_row}.
+ * n_tok in [1, 8], d % 512 == 0.
+ */
+size_t hsmoe_lm_head_workspace_size(int64_t n_tok, int64_t vocab);
+int hsmoe_lm_head_accept(const void* h_dev, const void* lm_head_dev, int64_t n_tok, int64_t d, int64_t vocab,
+                         const int64_t* ids_dev, void* logits_out_dev, int64_t* pred_out_dev,
+                         int64_t* result_out_dev, void* workspace_dev, size_t workspace_bytes,
+                         hsmoe_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * RMSNorm of bf16 rows with a bf16 weight (reference src/home_seek/utils.py:6-9):
+ *   out[r] = bf16(float(w) * (float(x[r]) * rsqrt(mean(float(x[r])^2) + eps)))
+ */
+int hsmoe_rms_norm(const void* x_dev, const void* w_dev, int64_t rows, int64_t d, float eps, void* out_dev,
+                   hsmoe_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Synthetic data generators (counter-based, reproducible on the host): value i
+ * of a stream is derived from r = splitmix64 output number i+1 for seed `key`.
+ * These have no counterpart in the reference (which loads a checkpoint); they
+ * fill the HBM expert store and the inputs of the benchmarks.
+ */
+int hsmoe_gen_bytes(uint64_t key, int64_t n, void* out_dev, hsmoe_stream_t stream);
+int hsmoe_gen_e4m3(uint64_t key, int64_t n, void* out_dev, hsmoe_stream_t stream);
+int hsmoe_gen_e8m0(uint64_t key, int64_t n, int lo, int span, void* out_dev, hsmoe_stream_t stream);
+int hsmoe_gen_normal(uint64_t key, int64_t n, float mean, float std, int as_bf16, void* out_dev,
+                     hsmoe_stream_t stream);
+int hsmoe_gen_uniform(uint64_t key, int64_t n, float lo, float hi, float mul, float* out_dev,
+                      hsmoe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HSMOE_H_ */

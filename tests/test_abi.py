@@ -1,0 +1,38 @@
+"""The C-ABI library loads and exports every declared entry point (no GPU needed)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _declared():
+    text = (ROOT / "include" / "hsmoe.h").read_text()
+    return sorted(set(re.findall(r"^(?:int|size_t|const char\*|void)\s+(hsmoe_\w+)\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    from home_seek_amd import _lib
+    assert set(_declared()) == set(_lib.exported_symbols())
+
+
+def test_library_exports_every_symbol():
+    handle = ctypes.CDLL(str(ROOT / "home-seek_amd" / "libhsmoe.so"))
+    for name in _declared():
+        assert hasattr(handle, name), name
+
+
+def test_version_and_error_paths():
+    from home_seek_amd import _lib
+    L = _lib.lib()
+    assert L.hsmoe_version() == 1
+    rc = L.hsmoe_fp4_dequant_bf16(None, None, 0, 1, 32, 16, 1, None, 32, None)
+    assert rc == -1 and b"null" in L.hsmoe_last_error()
+    rc = L.hsmoe_moe_decode(1, 9, 512, 512, 1, 1, 6, 1, 256, 0, None, 10.0, None, 1, 1, 1 << 20, None)
+    assert rc == -2 and b"m <= 8" in L.hsmoe_last_error()
+    rc = L.hsmoe_lm_head_accept(4096, 4096, 3, 4096, 129280, 4096, None, 4096, 4096, None, 0, None)
+    assert rc == -4
+    with pytest.raises(_lib.HsmoeError):
+        _lib.check(rc, "lm_head")
