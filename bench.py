@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-extras", action="store_true", help="skip the M=3 and lm_head side measurements")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="finish with 3 copies of a 256 MiB buffer (known bytes) to scale PMC byte counters")
     return ap.parse_args()
 
 
@@ -141,6 +143,10 @@ def main():
     us_stage2 = stage_graph(2)
     stage1_bytes = K * GATE_UP_BYTES + SHARED_GATE_UP + D * 2 + (K + 1) * 2 * I * 2
     stage2_bytes = K * DOWN_BYTES + SHARED_DOWN + (K + 1) * 2 * I * 2 + D * 6
+    traffic = None
+    pmc = ROOT / "profiles" / "moe_gate_up_kernel_m1_pmc.json"
+    if pmc.exists():  # HBM bytes per launch from the committed rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE runs
+        traffic = json.loads(pmc.read_text()).get("traffic_bytes_per_launch")
     ach1 = stage1_bytes / (us_stage1 * 1e-6) / 1e9
     ach2 = stage2_bytes / (us_stage2 * 1e-6) / 1e9
 
@@ -183,7 +189,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(ach1 / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "algorithmic_bytes_per_launch": stage1_bytes,
             "avg_launch_us": round(us_stage1, 3),
             "stage2": {"kernel": "moe_down_kernel", "achieved": round(ach2, 1), "avg_launch_us": round(us_stage2, 3),
@@ -192,6 +198,12 @@ def main():
         "cpu_baseline": cpu,
     }
     line.update(extras)
+    if args.calib_copy:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     print(json.dumps(line))
 
 

@@ -33,7 +33,7 @@ namespace {
 constexpr int kMaxTok = 8;
 constexpr int kMaxCand = 128;  // m * top_k
 constexpr int kP1Waves = 4;
-constexpr int kP2Waves = 16;
+constexpr int kP2Waves = 4;
 
 struct DecodeParams {
   const uint16_t* x;      // bf16 [m, d]
@@ -42,6 +42,8 @@ struct DecodeParams {
   const uint64_t* table;  // [n_experts][6]
   const uint64_t* shared; // [6] or null
   uint16_t* act;          // bf16 [slots][2m][i]
+  float* part;            // fp32 [slots][m][d] per-slot partial outputs
+  unsigned* counters;     // [d / 64] arrival counters (zero between calls)
   float* out_f32;         // [m, d] or null
   uint16_t* out_bf16;     // [m, d] or null
   int64_t n_experts;
@@ -90,106 +92,110 @@ __device__ void build_plan(const DecodeParams& p, Plan& plan, int* s_cand, int* 
 // expert is e4m3 with fp32 128x128 block scales, or bf16 likewise.
 enum Fmt : int { kFp4E8M0 = 0, kFp4F32 = 1, kFp8Block = 2, kBf16 = 3 };
 
-// One 128-column step of one matrix row as seen by lane (r, g): the columns
-// 128*st + 32g .. +32 of row `row` (a K-column matrix).  MFMA j of the step
-// uses columns +8j .. +8j+7, so the 4 lanes of a row cover 128 contiguous
-// columns per step.
-template <int F>
-struct Raw;
-template <>
-struct Raw<kFp4E8M0> { uint4 a; uint32_t e; };
-template <>
-struct Raw<kFp4F32> { uint4 a; float s; };
-template <>
-struct Raw<kFp8Block> { uint4 a, b; float s; };
-template <>
-struct Raw<kBf16> { uint4 a, b, c, d; };
+// A "step" is 128 consecutive columns of one weight row.  Lane (r, g) of a
+// wave owns columns 128*st + 32g .. +32 of row r: the 4 lanes of a row read
+// the step's bytes contiguously, and MFMA j of the step uses the lane's
+// columns +8j .. +8j+7 (so its k-slot 8g+jj is column 128*st + 32g + 8j + jj).
+// Batch<F, kB> holds the raw loads of kB consecutive steps; nothing is
+// decoded until every load of the batch has been issued.
+template <int F, int kB>
+struct Batch;
 
-template <int F>
-__device__ __forceinline__ Raw<F> load_step(const uint64_t w, const uint64_t sc, int64_t row, int64_t k, int64_t st,
-                                            int g) {
-  Raw<F> r;
-  if constexpr (F == kFp4E8M0 || F == kFp4F32) {
-    r.a = *reinterpret_cast<const uint4*>((const uint8_t*)w + row * (k / 2) + st * 64 + g * 16);
-    const int64_t si = row * (k / 32) + st * 4 + g;
-    if constexpr (F == kFp4E8M0)
-      r.e = ((const uint8_t*)sc)[si];
-    else
-      r.s = ((const float*)sc)[si];
-  } else if constexpr (F == kFp8Block) {
-    const uint8_t* b = (const uint8_t*)w + row * k + st * 128 + g * 32;
-    r.a = *reinterpret_cast<const uint4*>(b);
-    r.b = *reinterpret_cast<const uint4*>(b + 16);
-    r.s = ((const float*)sc)[(row / 128) * (k / 128) + st];
-  } else {
-    const uint4* b = reinterpret_cast<const uint4*>((const uint16_t*)w + row * k + st * 128 + g * 32);
-    r.a = b[0];
-    r.b = b[1];
-    r.c = b[2];
-    r.d = b[3];
+template <int kB>
+struct Batch<kFp4E8M0, kB> {
+  uint4 a[kB];
+  uint4 sq[kB >= 4 ? kB / 4 : 1];  // kB >= 4: 16 scale bytes per 4 steps (bytes 4b..4b+3 = step b)
+  uint32_t sb[kB];                 // kB < 4: one scale byte per step
+  __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
+    const uint8_t* base = (const uint8_t*)w + row * (k / 2) + st * 64 + g * 16;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) a[b] = *reinterpret_cast<const uint4*>(base + b * 64);
+    const uint8_t* sp = (const uint8_t*)sc + row * (k / 32) + st * 4;
+    if constexpr (kB >= 4) {
+#pragma unroll
+      for (int q = 0; q < kB / 4; ++q) sq[q] = *reinterpret_cast<const uint4*>(sp + 16 * q);
+    } else {
+#pragma unroll
+      for (int b = 0; b < kB; ++b) sb[b] = sp[4 * b + g];
+    }
   }
-  return r;
-}
+  __device__ __forceinline__ bf16x8 frag(int b, int j, int g) const {
+    const uint4& q = a[b];
+    const uint32_t dw = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
+    uint32_t e;
+    if constexpr (kB >= 4) {
+      const uint4& s4 = sq[b / 4];
+      const int d = b & 3;
+      const uint32_t word = d == 0 ? s4.x : d == 1 ? s4.y : d == 2 ? s4.z : s4.w;
+      e = (word >> (8 * g)) & 0xffu;
+    } else {
+      e = sb[b];
+    }
+    return fp4x8_to_bf16_e8m0(dw, e8m0_as_f32(e));
+  }
+};
 
-template <int F>
-__device__ __forceinline__ bf16x8 frag(const Raw<F>& r, int j) {
-  if constexpr (F == kFp4E8M0 || F == kFp4F32) {
-    const uint32_t dw = j == 0 ? r.a.x : j == 1 ? r.a.y : j == 2 ? r.a.z : r.a.w;
-    if constexpr (F == kFp4E8M0)
-      return fp4x8_to_bf16_e8m0(dw, e8m0_as_f32(r.e));
-    else
-      return fp4x8_to_bf16_f32(dw, r.s);
-  } else if constexpr (F == kFp8Block) {
-    const uint4& q = j < 2 ? r.a : r.b;
+template <int kB>
+struct Batch<kFp4F32, kB> {
+  uint4 a[kB];
+  float s[kB];
+  __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
+    const uint8_t* base = (const uint8_t*)w + row * (k / 2) + st * 64 + g * 16;
+    const float* sp = (const float*)sc + row * (k / 32) + st * 4 + g;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      a[b] = *reinterpret_cast<const uint4*>(base + b * 64);
+      s[b] = sp[4 * b];
+    }
+  }
+  __device__ __forceinline__ bf16x8 frag(int b, int j, int) const {
+    const uint4& q = a[b];
+    const uint32_t dw = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
+    return fp4x8_to_bf16_f32(dw, s[b]);
+  }
+};
+
+template <int kB>
+struct Batch<kFp8Block, kB> {
+  uint4 a[kB], c[kB];
+  float s[kB];
+  __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
+    const uint8_t* base = (const uint8_t*)w + row * k + st * 128 + g * 32;
+    const float* sp = (const float*)sc + (row / 128) * (k / 128) + st;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      a[b] = *reinterpret_cast<const uint4*>(base + b * 128);
+      c[b] = *reinterpret_cast<const uint4*>(base + b * 128 + 16);
+      s[b] = sp[b];
+    }
+  }
+  __device__ __forceinline__ bf16x8 frag(int b, int j, int) const {
+    const uint4& q = j < 2 ? a[b] : c[b];
     const uint32_t d0 = (j & 1) ? q.z : q.x, d1 = (j & 1) ? q.w : q.y;
     bf16x8 f;
-    fp8x4_to_bf16(d0, r.s, f, 0);
-    fp8x4_to_bf16(d1, r.s, f, 1);
+    fp8x4_to_bf16(d0, s[b], f, 0);
+    fp8x4_to_bf16(d1, s[b], f, 1);
     return f;
-  } else {
-    const uint4& q = j == 0 ? r.a : j == 1 ? r.b : j == 2 ? r.c : r.d;
-    return __builtin_bit_cast(bf16x8, q);
   }
-}
+};
 
-template <int F>
-constexpr int batch_steps() {
-  return (F == kFp4E8M0 || F == kFp4F32) ? 4 : 2;
-}
-
-// ---------------------------------------------------------------- phase 1
-// Streams rows r0..r0+15 of W1 and W3 over steps [st0, st1).  The B operand
-// lane (c = token, g) holds x[c][128*st + 32g + 8j ..], matching frag().
-template <int F>
-__device__ __forceinline__ void gate_up(const DecodeParams& p, const uint64_t* ent, int r0, int st0, int st1,
-                                        f32x4& ag, f32x4& au) {
-  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4, c = lane & 15;
-  const int64_t row = r0 + r;
-  const uint16_t* xr = p.x + (int64_t)c * p.d + g * 32;
-  const bool xon = c < p.m;
-  constexpr int kB = batch_steps<F>();
-  for (int st = st0; st < st1; st += kB) {
-    Raw<F> a1[kB], a3[kB];
+template <int kB>
+struct Batch<kBf16, kB> {
+  uint4 a[kB][4];
+  __device__ __forceinline__ void load(uint64_t w, uint64_t, int64_t row, int64_t k, int64_t st, int g) {
+    const uint4* base = reinterpret_cast<const uint4*>((const uint16_t*)w + row * k + st * 128 + g * 32);
 #pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      if (st + b < st1) {
-        a1[b] = load_step<F>(ent[0], ent[1], row, p.d, st + b, g);
-        a3[b] = load_step<F>(ent[2], ent[3], row, p.d, st + b, g);
-      }
-    }
+    for (int b = 0; b < kB; ++b)
 #pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      if (st + b < st1) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          bf16x8 xf = {};
-          if (xon) xf = *reinterpret_cast<const bf16x8*>(xr + (int64_t)(st + b) * 128 + 8 * j);
-          ag = mfma16x16x32(frag<F>(a1[b], j), xf, ag);
-          au = mfma16x16x32(frag<F>(a3[b], j), xf, au);
-        }
-      }
-    }
+      for (int j = 0; j < 4; ++j) a[b][j] = base[b * 16 + j];
   }
+  __device__ __forceinline__ bf16x8 frag(int b, int j, int) const { return __builtin_bit_cast(bf16x8, a[b][j]); }
+};
+
+// Steps per batch (register budget: ~64 VGPRs of raw weights per matrix).
+template <int F>
+constexpr int max_batch() {
+  return (F == kFp4E8M0 || F == kFp4F32) ? 8 : (F == kFp8Block ? 4 : 2);
 }
 
 __device__ __forceinline__ int slot_format(const DecodeParams& p, const uint64_t* ent, bool is_shared) {
@@ -197,7 +203,51 @@ __device__ __forceinline__ int slot_format(const DecodeParams& p, const uint64_t
   return ent[1] ? p.scale_fmt : kBf16;
 }
 
+// B operand from an LDS tile laid out [16 columns][kcols] bf16: lane (c, g)
+// takes columns 128*st + 32g + 8j .. +8 of tile column c (zero when c >= ncol).
+__device__ __forceinline__ bf16x8 lds_frag(const uint16_t* tile, int kcols, int c, int g, int st, int j, int ncol) {
+  bf16x8 z = {};
+  if (c >= ncol) return z;
+  return *reinterpret_cast<const bf16x8*>(tile + c * kcols + st * 128 + g * 32 + 8 * j);
+}
+
+// ---------------------------------------------------------------- phase 1
+// Wave w of the block streams rows r0..r0+15 of W1 and W3 over its quarter of
+// the d/128 steps; x [m][d] sits in LDS.
+template <int F, int kB>
+__device__ __forceinline__ void gate_up(const DecodeParams& p, const uint64_t* ent, const uint16_t* xs, int r0,
+                                        int st0, int st1, f32x4& ag, f32x4& au) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int64_t row = r0 + r;
+  for (int st = st0; st < st1; st += kB) {
+    Batch<F, kB> b1, b3;
+    b1.load(ent[0], ent[1], row, p.d, st, g);
+    b3.load(ent[2], ent[3], row, p.d, st, g);
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bf16x8 xf = lds_frag(xs, p.d, r, g, st + b, j, p.m);
+        ag = mfma16x16x32(b1.frag(b, j, g), xf, ag);
+        au = mfma16x16x32(b3.frag(b, j, g), xf, au);
+      }
+    }
+  }
+}
+
+template <int F>
+__device__ __forceinline__ void gate_up_dispatch(const DecodeParams& p, const uint64_t* ent, const uint16_t* xs,
+                                                 int r0, int st0, int st1, f32x4& ag, f32x4& au) {
+  const int n = st1 - st0;
+  constexpr int kMax = max_batch<F>();
+  if (n % kMax == 0) gate_up<F, kMax>(p, ent, xs, r0, st0, st1, ag, au);
+  else if (kMax > 4 && n % 4 == 0) gate_up<F, (kMax > 4 ? 4 : 1)>(p, ent, xs, r0, st0, st1, ag, au);
+  else if (kMax > 2 && n % 2 == 0) gate_up<F, (kMax > 2 ? 2 : 1)>(p, ent, xs, r0, st0, st1, ag, au);
+  else gate_up<F, 1>(p, ent, xs, r0, st0, st1, ag, au);
+}
+
 __global__ void __launch_bounds__(64 * kP1Waves) moe_gate_up_kernel(DecodeParams p) {
+  extern __shared__ __align__(16) uint16_t xs[];  // [m][d] bf16
   __shared__ Plan plan;
   __shared__ int s_cand[kMaxCand];
   __shared__ int s_first[kMaxCand];
@@ -211,6 +261,10 @@ __global__ void __launch_bounds__(64 * kP1Waves) moe_gate_up_kernel(DecodeParams
   const uint64_t* ent = is_shared ? p.shared : p.table + (int64_t)plan.eid[s] * 6;
   const int r0 = blockIdx.x * 16;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // x -> LDS (16 bytes per thread per pass)
+  const int n16 = p.m * p.d / 8;
+  for (int q = threadIdx.x; q < n16; q += blockDim.x)
+    reinterpret_cast<uint4*>(xs)[q] = reinterpret_cast<const uint4*>(p.x)[q];
   if (threadIdx.x < p.m) {
     float w = 0.0f;
     if (is_shared) {
@@ -222,14 +276,15 @@ __global__ void __launch_bounds__(64 * kP1Waves) moe_gate_up_kernel(DecodeParams
     }
     s_wt[threadIdx.x] = w;
   }
+  __syncthreads();
   const int per = (p.d / 128) / kP1Waves;
   const int st0 = wave * per, st1 = st0 + per;
   f32x4 ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
   switch (slot_format(p, ent, is_shared)) {
-    case kFp4E8M0: gate_up<kFp4E8M0>(p, ent, r0, st0, st1, ag, au); break;
-    case kFp4F32: gate_up<kFp4F32>(p, ent, r0, st0, st1, ag, au); break;
-    case kFp8Block: gate_up<kFp8Block>(p, ent, r0, st0, st1, ag, au); break;
-    default: gate_up<kBf16>(p, ent, r0, st0, st1, ag, au); break;
+    case kFp4E8M0: gate_up_dispatch<kFp4E8M0>(p, ent, xs, r0, st0, st1, ag, au); break;
+    case kFp4F32: gate_up_dispatch<kFp4F32>(p, ent, xs, r0, st0, st1, ag, au); break;
+    case kFp8Block: gate_up_dispatch<kFp8Block>(p, ent, xs, r0, st0, st1, ag, au); break;
+    default: gate_up_dispatch<kBf16>(p, ent, xs, r0, st0, st1, ag, au); break;
   }
   // D[4*(lane/16) + q][lane%16] lives in element q of lane
 #pragma unroll
@@ -262,80 +317,109 @@ __global__ void __launch_bounds__(64 * kP1Waves) moe_gate_up_kernel(DecodeParams
 }
 
 // ---------------------------------------------------------------- phase 2
-// Unit = (slot s, 512 columns from k0) of 16 rows of W2; the B operand lane
-// (c, g) holds act[s][c][k0 + 128st + 32g + 8j ..] (c < m: hi, m <= c < 2m: lo).
-template <int F>
-__device__ __forceinline__ void down_unit(const DecodeParams& p, const uint64_t* ent, int s, int r0, int k0,
+// Block (row group rg of 64 output rows, slot s): the slot's activation tile
+// act[s] ([2m][i] bf16: hi then lo columns) is staged in LDS; wave w streams
+// rows rg*64 + 16w .. +16 of W2 over all i/128 steps and writes the fp32
+// partial sum of its rows for this slot.  The last block of a row group to
+// finish (atomic arrival count) adds the slots' partials in slot order and
+// writes the output, then re-arms the counter: deterministic, and nothing
+// ever waits on another block.
+template <int F, int kB>
+__device__ __forceinline__ void down_rows(const DecodeParams& p, const uint64_t* ent, const uint16_t* as, int r0,
                                           f32x4& acc) {
-  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4, c = lane & 15;
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int64_t row = r0 + r;
-  const bool bon = c < 2 * p.m;
-  const uint16_t* ar = p.act + ((int64_t)s * 2 * p.m + c) * p.i + k0 + g * 32;
-  constexpr int kB = batch_steps<F>();
-  const int st0 = k0 / 128;
+  const int n = p.i / 128;
+  for (int st = 0; st < n; st += kB) {
+    Batch<F, kB> bw;
+    bw.load(ent[4], ent[5], row, p.i, st, g);
 #pragma unroll
-  for (int sb = 0; sb < 4; sb += kB) {
-    Raw<F> a[kB];
+    for (int b = 0; b < kB; ++b)
 #pragma unroll
-    for (int b = 0; b < kB; ++b) a[b] = load_step<F>(ent[4], ent[5], row, p.i, st0 + sb + b, g);
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bf16x8 bf = {};
-        if (bon) bf = *reinterpret_cast<const bf16x8*>(ar + (sb + b) * 128 + 8 * j);
-        acc = mfma16x16x32(frag<F>(a[b], j), bf, acc);
-      }
-    }
+      for (int j = 0; j < 4; ++j) acc = mfma16x16x32(bw.frag(b, j, g), lds_frag(as, p.i, r, g, st + b, j, 2 * p.m), acc);
   }
+}
+
+template <int F>
+__device__ __forceinline__ void down_dispatch(const DecodeParams& p, const uint64_t* ent, const uint16_t* as, int r0,
+                                              f32x4& acc) {
+  const int n = p.i / 128;
+  constexpr int kMax = (F == kFp4E8M0 || F == kFp4F32) ? 16 : max_batch<F>();
+  if (n % kMax == 0) down_rows<F, kMax>(p, ent, as, r0, acc);
+  else if (kMax > 8 && n % 8 == 0) down_rows<F, (kMax > 8 ? 8 : 1)>(p, ent, as, r0, acc);
+  else if (kMax > 4 && n % 4 == 0) down_rows<F, (kMax > 4 ? 4 : 1)>(p, ent, as, r0, acc);
+  else if (kMax > 2 && n % 2 == 0) down_rows<F, (kMax > 2 ? 2 : 1)>(p, ent, as, r0, acc);
+  else down_rows<F, 1>(p, ent, as, r0, acc);
 }
 
 __global__ void __launch_bounds__(64 * kP2Waves) moe_down_kernel(DecodeParams p) {
+  extern __shared__ __align__(16) uint16_t as[];  // [2m][i] bf16
   __shared__ Plan plan;
   __shared__ int s_cand[kMaxCand];
   __shared__ int s_first[kMaxCand];
-  __shared__ float red[kP2Waves][256];
-  __shared__ float tot[256];
+  __shared__ int s_last;
   build_plan(p, plan, s_cand, s_first);
   const int n_slots = plan.n_routed + (p.shared ? 1 : 0);
-  const int r0 = blockIdx.x * 16;
+  const int s = blockIdx.y;
+  if (s >= n_slots) return;  // not counted: the arrival target is n_slots
+  const bool is_shared = s == plan.n_routed;
+  const uint64_t* ent = is_shared ? p.shared : p.table + (int64_t)plan.eid[s] * 6;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int ups = p.i / 512;
-  const int n_units = n_slots * ups;
+  const int r0 = blockIdx.x * (16 * kP2Waves) + 16 * wave;
+  const int n16 = 2 * p.m * p.i / 8;
+  const uint4* src = reinterpret_cast<const uint4*>(p.act + (int64_t)s * 2 * p.m * p.i);
+  for (int q = threadIdx.x; q < n16; q += blockDim.x) reinterpret_cast<uint4*>(as)[q] = src[q];
+  __syncthreads();
   f32x4 acc = {0, 0, 0, 0};
-  for (int u = wave; u < n_units; u += kP2Waves) {
-    const int s = u / ups, k0 = (u - s * ups) * 512;
-    const bool is_shared = s == plan.n_routed;
-    const uint64_t* ent = is_shared ? p.shared : p.table + (int64_t)plan.eid[s] * 6;
-    switch (slot_format(p, ent, is_shared)) {
-      case kFp4E8M0: down_unit<kFp4E8M0>(p, ent, s, r0, k0, acc); break;
-      case kFp4F32: down_unit<kFp4F32>(p, ent, s, r0, k0, acc); break;
-      case kFp8Block: down_unit<kFp8Block>(p, ent, s, r0, k0, acc); break;
-      default: down_unit<kBf16>(p, ent, s, r0, k0, acc); break;
-    }
+  switch (slot_format(p, ent, is_shared)) {
+    case kFp4E8M0: down_dispatch<kFp4E8M0>(p, ent, as, r0, acc); break;
+    case kFp4F32: down_dispatch<kFp4F32>(p, ent, as, r0, acc); break;
+    case kFp8Block: down_dispatch<kFp8Block>(p, ent, as, r0, acc); break;
+    default: down_dispatch<kBf16>(p, ent, as, r0, acc); break;
   }
+  // lane (col = lane%16) holds rows 4*(lane/16)+q; column t (hi) + column m+t (lo)
+  // of token t are combined through the lane that owns column t.
+  // Cross-block handoff without cache flushes: partials are written with
+  // agent-scope (L2-bypassing, sc1) stores, each wave waits for its stores to
+  // complete before the barrier, and only then is the arrival counter bumped;
+  // the last block reads the partials with agent-scope loads.
+  float* part = p.part + (int64_t)s * p.m * p.d;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) red[wave][(4 * (lane >> 4) + q) * 16 + (lane & 15)] = acc[q];
+  for (int q = 0; q < 4; ++q) {
+    const int col = lane & 15;
+    const float lo = __shfl(acc[q], (lane & 48) | ((col + p.m) & 15), 64);
+    if (col < p.m)
+      __hip_atomic_store(part + (int64_t)col * p.d + r0 + 4 * (lane >> 4) + q, __fadd_rn(acc[q], lo), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x < 256) {
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(&p.counters[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (unsigned)(n_slots - 1);
+  __syncthreads();
+  if (!s_last) return;
+  const int rows = 16 * kP2Waves;
+  for (int q = threadIdx.x; q < rows * p.m; q += blockDim.x) {
+    const int t = q / rows, d = blockIdx.x * rows + (q - t * rows);
     float v = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kP2Waves; ++w) v = __fadd_rn(v, red[w][threadIdx.x]);
-    tot[threadIdx.x] = v;
+    for (int ss = 0; ss < n_slots; ++ss)
+      v = __fadd_rn(v, __hip_atomic_load(p.part + ((int64_t)ss * p.m + t) * p.d + d, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT));
+    const int64_t o = (int64_t)t * p.d + d;
+    if (p.out_f32) p.out_f32[o] = v;
+    if (p.out_bf16) p.out_bf16[o] = (uint16_t)f32_to_bf16_bits(v);
   }
-  __syncthreads();
-  if (threadIdx.x < 256) {
-    const int row = threadIdx.x >> 4, t = threadIdx.x & 15;
-    if (t < p.m) {
-      const float v = __fadd_rn(tot[row * 16 + t], tot[row * 16 + p.m + t]);
-      const int64_t o = (int64_t)t * p.d + r0 + row;
-      if (p.out_f32) p.out_f32[o] = v;
-      if (p.out_bf16) p.out_bf16[o] = (uint16_t)f32_to_bf16_bits(v);
-    }
-  }
+  if (threadIdx.x == 0) __hip_atomic_store(&p.counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-size_t act_bytes(int64_t m, int64_t i, int top_k) { return (size_t)(m * top_k + 1) * 2 * m * i * 2; }
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+// Workspace layout: [arrival counters, fixed 4 KiB at offset 0 | act | part].
+// The counters sit at the same place for every shape and every call leaves
+// them at zero, so calls of different shapes can share one workspace.
+constexpr size_t kCounterBytes = 4096;  // d / 64 <= 1024 counters
+size_t act_bytes(int64_t m, int64_t i, int top_k) { return align256((size_t)(m * top_k + 1) * 2 * m * i * 2); }
+size_t part_bytes(int64_t m, int64_t d, int top_k) { return align256((size_t)(m * top_k + 1) * m * d * 4); }
 
 }  // namespace
 }  // namespace hsmoe
@@ -343,9 +427,8 @@ size_t act_bytes(int64_t m, int64_t i, int top_k) { return (size_t)(m * top_k + 
 using namespace hsmoe;
 
 extern "C" size_t hsmoe_moe_decode_workspace_size(int64_t m, int64_t d, int64_t i, int top_k) {
-  (void)d;
-  if (m < 1 || i < 1 || top_k < 1) return 0;
-  return (act_bytes(m, i, top_k) + 255) / 256 * 256;
+  if (m < 1 || i < 1 || d < 1 || top_k < 1) return 0;
+  return kCounterBytes + act_bytes(m, i, top_k) + part_bytes(m, d, top_k);
 }
 
 static int moe_decode_launch(const void* x, int64_t m, int64_t d, int64_t i, const int64_t* topk_idx,
@@ -360,20 +443,24 @@ static int moe_decode_launch(const void* x, int64_t m, int64_t d, int64_t i, con
   if (m < 1 || m > kMaxTok || top_k < 1 || top_k > 16 || m * top_k > kMaxCand)
     return fail(HSMOE_ERR_SHAPE, "%s: need 1 <= m <= 8 and 1 <= top_k <= 16 (got m=%lld top_k=%d)", name,
                 (long long)m, top_k);
-  if (d % 512 != 0 || i % 512 != 0 || d <= 0 || i <= 0)
-    return fail(HSMOE_ERR_SHAPE, "%s: d and i must be positive multiples of 512 (d=%lld i=%lld)", name,
+  if (d % 512 != 0 || i % 512 != 0 || d <= 0 || i <= 0 || (size_t)(d / 64) * 4 > kCounterBytes)
+    return fail(HSMOE_ERR_SHAPE, "%s: d and i must be positive multiples of 512, d <= 65536 (d=%lld i=%lld)", name,
                 (long long)d, (long long)i);
   if (!aligned(x, 16)) return fail(HSMOE_ERR_SHAPE, "%s: x must be 16-byte aligned", name);
   const size_t need = hsmoe_moe_decode_workspace_size(m, d, i, top_k);
-  if (!workspace || workspace_bytes < need || !aligned(workspace, 16))
-    return fail(HSMOE_ERR_WORKSPACE, "%s: workspace of %zu bytes (16-byte aligned) needed", name, need);
+  if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+    return fail(HSMOE_ERR_WORKSPACE, "%s: zero-filled workspace of %zu bytes (256-byte aligned) needed", name, need);
+  if (m * d * 2 > 65536 || 2 * m * i * 2 > 65536)
+    return fail(HSMOE_ERR_SHAPE, "%s: m*d and 2*m*i tiles must fit in 64 KiB of LDS", name);
   DecodeParams p;
   p.x = (const uint16_t*)x;
   p.idx = topk_idx;
   p.wts = topk_w;
   p.table = expert_table;
   p.shared = shared;
-  p.act = (uint16_t*)workspace;
+  p.counters = (unsigned*)workspace;
+  p.act = (uint16_t*)((char*)workspace + kCounterBytes);
+  p.part = (float*)((char*)workspace + kCounterBytes + act_bytes(m, i, top_k));
   p.out_f32 = out_f32;
   p.out_bf16 = (uint16_t*)out_bf16;
   p.n_experts = n_experts;
@@ -386,12 +473,14 @@ static int moe_decode_launch(const void* x, int64_t m, int64_t d, int64_t i, con
   const unsigned max_slots = (unsigned)(m * top_k + (shared ? 1 : 0));
   hipStream_t st = (hipStream_t)stream;
   if (stages & 1) {
-    hipLaunchKernelGGL(moe_gate_up_kernel, dim3((unsigned)(i / 16), max_slots), dim3(64 * kP1Waves), 0, st, p);
+    hipLaunchKernelGGL(moe_gate_up_kernel, dim3((unsigned)(i / 16), max_slots), dim3(64 * kP1Waves),
+                       (size_t)(m * d * 2), st, p);
     int rc = check_launch(name);
     if (rc) return rc;
   }
   if (stages & 2) {
-    hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)(d / 16)), dim3(64 * kP2Waves), 0, st, p);
+    hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)(d / (16 * kP2Waves)), max_slots), dim3(64 * kP2Waves),
+                       (size_t)(2 * m * i * 2), st, p);
     return check_launch(name);
   }
   return HSMOE_OK;

@@ -85,25 +85,24 @@ __global__ void __launch_bounds__(64 * kWaves)
     if (lane == 0) s_key[wave][t] = k;
   }
   __syncthreads();
+  // Argmax keys and the arrival counter are agent-scope atomics (coherent across
+  // XCDs); each block waits for its atomics to complete before it arrives.
   if (threadIdx.x < kTok) {
     unsigned long long k = 0;
 #pragma unroll
     for (int q = 0; q < kWaves; ++q) k = s_key[q][threadIdx.x] > k ? s_key[q][threadIdx.x] : k;
-    atomicMax(&ws->key[threadIdx.x], k);
+    __hip_atomic_fetch_max(&ws->key[threadIdx.x], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    unsigned int prev = atomicAdd(&ws->done, 1u);
-    s_last = prev == gridDim.x - 1;
-  }
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(&ws->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
   __syncthreads();
   if (!s_last || threadIdx.x != 0) return;
-  __threadfence();
   int64_t pred[kTok];
 #pragma unroll
   for (int t = 0; t < kTok; ++t) {
-    unsigned long long k = atomicExch(&ws->key[t], 0ull);
+    const unsigned long long k = __hip_atomic_exchange(&ws->key[t], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     pred[t] = (int64_t)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
     pred_out[t] = pred[t];
   }
@@ -114,7 +113,7 @@ __global__ void __launch_bounds__(64 * kWaves)
   }
   result_out[0] = n_acc;
   result_out[1] = n_acc;
-  atomicExch(&ws->done, 0u);
+  __hip_atomic_store(&ws->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int kTok>

@@ -79,7 +79,7 @@ int hsmoe_fp8_dequant_bf16(const void* data_dev, const float* scale_dev, int64_t
  *   w[m, j]     = score[idx[m, j]] / max(sum_j score[idx[m, j]], 1e-20) * scaling
  * x: bf16 [m, d]; gate_w: bf16 [n_experts, d]; bias: fp32 [n_experts] or NULL.
  * idx_out: int64 [m, top_k]; w_out: fp32 [m, top_k]; logits_out: bf16
- * [m, n_experts] or NULL.  n_experts <= 1024, top_k <= 16, d % 256 == 0.
+ * [m, n_experts] or NULL.  n_experts <= 1024, top_k <= 16, d % 512 == 0, d <= 8192.
  */
 size_t hsmoe_router_workspace_size(int64_t m, int64_t n_experts);
 int hsmoe_router_topk(const void* x_dev, const void* gate_w_dev, const float* bias_dev, int64_t m, int64_t d,

@@ -87,8 +87,8 @@ def test_router_ids_bit_exact(dev, m):
 
 
 def test_router_ties_and_no_bias(dev):
-    x = torch.ones(2, 256, dtype=torch.bfloat16, device=dev)
-    gate = torch.full((64, 256), 0.5, dtype=torch.bfloat16, device=dev)
+    x = torch.ones(2, 512, dtype=torch.bfloat16, device=dev)
+    gate = torch.full((64, 512), 0.5, dtype=torch.bfloat16, device=dev)
     idx, w = ops.router_topk(x, gate, None, 6, 1.5)
     assert idx.cpu().tolist() == [[0, 1, 2, 3, 4, 5]] * 2
     assert torch.allclose(w, torch.full_like(w, 0.25))

@@ -165,3 +165,20 @@ def test_shared_expert_ffn_bf16(layer, dev):
     out = fused_moe.SharedExpertFFN(D, I, 10.0).forward(x.reshape(1, 2, D), w1, w3, w2)
     ref = orc.expert_ffn_fp32(orc.to_np_bf16(x), sh["w1_bf16"], sh["w3_bf16"], sh["w2_bf16"], 10.0)
     assert_bf16_close(orc.bf16_to_f32(orc.to_np_bf16(out.reshape(2, D))), orc.bf16_to_f32(orc.f32_to_bf16(ref)))
+
+
+def test_workspace_reuse_across_shapes(layer, dev):
+    """Calls of different m share one workspace (largest first): every call must
+    still complete its cross-slot reduction (regression: arrival counters
+    placed at a shape-dependent offset read stale bytes)."""
+    store, gate, bias = layer
+    results = {}
+    for m in (8, 2, 5, 1):
+        x = synthetic.hidden(SEED, 700 + m, m, D, dev)
+        idx, w = ops.router_topk(x, gate, bias, K, 1.5)
+        out, _ = ops.moe_decode(x, idx, w, store.table(0), ops.SCALE_E8M0, store.shared_entry(0), 10.0, d=D, i=I)
+        results[m] = (x, idx, w, out)
+    for m, (x, idx, w, out) in results.items():
+        experts = {int(e): oracle_expert(int(e)) for e in np.unique(idx.cpu().numpy())}
+        ref = orc.moe_layer_fp32(orc.to_np_bf16(x), idx.cpu().numpy(), w.cpu().numpy(), experts, oracle_shared())
+        assert_bf16_close(orc.bf16_to_f32(orc.to_np_bf16(out)), orc.bf16_to_f32(orc.f32_to_bf16(ref)), f"m={m}")
