@@ -39,6 +39,8 @@ DOWN_BYTES = D * I // 2 + D * I // 32                      # w2 + scales
 SHARED_GATE_UP = 2 * I * D + 2 * (I // 128) * (D // 128) * 4
 SHARED_DOWN = D * I + (D // 128) * (I // 128) * 4
 ROUTER_BYTES = E * D * 2 + E * 4
+EXPERT_WEIGHT_BYTES = K * EXPERT_BYTES + SHARED_GATE_UP + SHARED_DOWN     # routed + shared expert weights
+LAYER_IO_BYTES = EXPERT_WEIGHT_BYTES + ROUTER_BYTES + 2 * D * 2             # + router weights, x in, out
 HBM_PEAK_GBS = 8000.0
 
 
@@ -54,6 +56,9 @@ def parse():
     ap.add_argument("--no-extras", action="store_true", help="skip the M=3 and lm_head side measurements")
     ap.add_argument("--calib-copy", action="store_true",
                     help="finish with 3 copies of a 256 MiB buffer (known bytes) to scale PMC byte counters")
+    ap.add_argument("--path", choices=("fused", "staged"), default="fused",
+                    help="fused: one persistent launch per layer (hsmoe_moe_layer_decode); "
+                         "staged: router, gate/up and down launches")
     return ap.parse_args()
 
 
@@ -81,7 +86,13 @@ def main():
     outs = [torch.empty(1, D, dtype=torch.bfloat16, device=dev) for _ in range(L)]
     torch.cuda.synchronize()
 
+    fused = args.path == "fused"
+
     def step(l):
+        if fused:
+            ops.moe_layer_decode(xs[l], routers[l][0], routers[l][1], tables[l], ops.SCALE_E8M0, shareds[l], I, K,
+                                 1.5, 10.0, out_bf16=outs[l], idx_out=idx_buf[l], w_out=w_buf[l])
+            return
         idx, w = ops.router_topk(xs[l], routers[l][0], routers[l][1], K, 1.5, out=(idx_buf[l], w_buf[l]))
         ops.moe_decode(xs[l], idx, w, tables[l], ops.SCALE_E8M0, shareds[l], 10.0, out_bf16=outs[l], d=D, i=I)
 
@@ -113,9 +124,12 @@ def main():
     wall = time.perf_counter() - t0
     ms_step = ev0.elapsed_time(ev1) / steps
     routed_gbs = K * EXPERT_BYTES / (ms_step * 1e-3) / 1e9
-    layer_bytes = K * EXPERT_BYTES + SHARED_GATE_UP + SHARED_DOWN + ROUTER_BYTES
 
-    # ---- dominant kernel: stage 1 (gate/up) alone, back-to-back in a graph
+    # ---- dominant kernel
+    # fused: a step is exactly one launch of moe_layer_kernel, so its average
+    # duration is the step graph's event time per step (events on the stream
+    # the graph replays on).  staged: stage 1 (gate/up) alone, back-to-back in
+    # a graph of its own.
     def stage_graph(stage):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(stream):
@@ -139,20 +153,32 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / (replays * L) * 1e3  # us per launch
 
-    us_stage1 = stage_graph(1)
-    us_stage2 = stage_graph(2)
-    stage1_bytes = K * GATE_UP_BYTES + SHARED_GATE_UP + D * 2 + (K + 1) * 2 * I * 2
-    stage2_bytes = K * DOWN_BYTES + SHARED_DOWN + (K + 1) * 2 * I * 2 + D * 6
+    pmc_name = "moe_layer_kernel_m1_pmc.json" if fused else "moe_gate_up_kernel_m1_pmc.json"
     traffic = None
-    pmc = ROOT / "profiles" / "moe_gate_up_kernel_m1_pmc.json"
+    pmc = ROOT / "profiles" / pmc_name
     if pmc.exists():  # HBM bytes per launch from the committed rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE runs
         traffic = json.loads(pmc.read_text()).get("traffic_bytes_per_launch")
-    ach1 = stage1_bytes / (us_stage1 * 1e-6) / 1e9
-    ach2 = stage2_bytes / (us_stage2 * 1e-6) / 1e9
+    if fused:
+        us_launch = ms_step * 1e3
+        kernel_bytes = LAYER_IO_BYTES
+        roof = {"kernel": "moe_layer_kernel (router + 6 routed FP4 + FP8 shared expert, one launch)"}
+    else:
+        us_launch = stage_graph(1)
+        us_stage2 = stage_graph(2)
+        kernel_bytes = K * GATE_UP_BYTES + SHARED_GATE_UP + D * 2 + (K + 1) * 2 * I * 2
+        stage2_bytes = K * DOWN_BYTES + SHARED_DOWN + (K + 1) * 2 * I * 2 + D * 6
+        roof = {"kernel": "moe_gate_up_kernel (stage 1)",
+                "stage2": {"kernel": "moe_down_kernel", "avg_launch_us": round(us_stage2, 3),
+                           "achieved": round(stage2_bytes / (us_stage2 * 1e-6) / 1e9, 1),
+                           "algorithmic_bytes_per_launch": stage2_bytes}}
+    ach = kernel_bytes / (us_launch * 1e-6) / 1e9
+    roof = {"bound": "hbm", **roof, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "algorithmic_bytes_per_launch": kernel_bytes,
+            "avg_launch_us": round(us_launch, 3)}
 
     extras = {}
     if not args.no_extras:
-        extras = side_measurements(torch, ops, synthetic, store, routers, tables, shareds, stream, args, L)
+        extras = side_measurements(torch, ops, synthetic, store, routers, tables, shareds, stream, args, L, fused)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -180,21 +206,11 @@ def main():
             "layers_rotated": L,
         },
         "pct_hbm_peak": round(100.0 * routed_gbs / HBM_PEAK_GBS, 2),
-        "full_layer_gbs": round(layer_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "expert_gbs": round(EXPERT_WEIGHT_BYTES / (ms_step * 1e-3) / 1e9, 1),
+        "full_layer_gbs": round(LAYER_IO_BYTES / (ms_step * 1e-3) / 1e9, 1),
+        "path": args.path,
         "wall_s_timed": round(wall, 3),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "moe_gate_up_kernel (stage 1)",
-            "achieved": round(ach1, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(ach1 / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "algorithmic_bytes_per_launch": stage1_bytes,
-            "avg_launch_us": round(us_stage1, 3),
-            "stage2": {"kernel": "moe_down_kernel", "achieved": round(ach2, 1), "avg_launch_us": round(us_stage2, 3),
-                       "algorithmic_bytes_per_launch": stage2_bytes},
-        },
+        "roofline": roof,
         "cpu_baseline": cpu,
     }
     line.update(extras)
@@ -207,7 +223,7 @@ def main():
     print(json.dumps(line))
 
 
-def side_measurements(torch, ops, synthetic, store, routers, tables, shareds, stream, args, L):
+def side_measurements(torch, ops, synthetic, store, routers, tables, shareds, stream, args, L, fused):
     """M=3 verify layer (per-token distinct routing) and the T=3 lm_head + acceptance kernel."""
     xs3 = [synthetic.hidden(args.seed, 2000 + l, 3, D, store.device) for l in range(L)]
     uniq = []
@@ -217,6 +233,10 @@ def side_measurements(torch, ops, synthetic, store, routers, tables, shareds, st
     outs = [torch.empty(3, D, dtype=torch.bfloat16, device=store.device) for _ in range(L)]
 
     def step3(l):
+        if fused:
+            ops.moe_layer_decode(xs3[l], routers[l][0], routers[l][1], tables[l], ops.SCALE_E8M0, shareds[l], I, K,
+                                 1.5, 10.0, out_bf16=outs[l])
+            return
         idx, w = ops.router_topk(xs3[l], routers[l][0], routers[l][1], K, 1.5)
         ops.moe_decode(xs3[l], idx, w, tables[l], ops.SCALE_E8M0, shareds[l], 10.0, out_bf16=outs[l], d=D, i=I)
 

@@ -40,6 +40,11 @@ _SIGNATURES = {
                                  _c_void_p, _f32, _c_void_p, _size, _c_void_p]),
     "hsmoe_moe_down": (_int, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _int, _c_void_p, _i64, _int,
                               _c_void_p, _c_void_p, _c_void_p, _c_void_p, _size, _c_void_p]),
+    "hsmoe_moe_layer_workspace_size": (_size, [_i64, _i64, _i64, _i64, _int]),
+    "hsmoe_moe_layer_decode": (_int, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _i64, _int, _f32, _c_void_p,
+                                      _int, _c_void_p, _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                      _c_void_p, _size, _c_void_p]),
+    "hsmoe_moe_layer_status_offset": (_size, []),
     "hsmoe_lm_head_workspace_size": (_size, [_i64, _i64]),
     "hsmoe_lm_head_accept": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
                                     _c_void_p, _c_void_p, _size, _c_void_p]),

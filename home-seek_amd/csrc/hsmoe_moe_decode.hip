@@ -26,6 +26,7 @@
 
 #include "hsmoe_common.h"
 #include "hsmoe_internal.h"
+#include "hsmoe_tiles.h"
 
 namespace hsmoe {
 namespace {
@@ -86,166 +87,6 @@ __device__ void build_plan(const DecodeParams& p, Plan& plan, int* s_cand, int* 
   __syncthreads();
 }
 
-// ---------------------------------------------------------------- weights
-// Weight formats of a slot.  Routed experts are FP4 with the call's scale
-// encoding, or bf16 when the table entry has no scale pointer; the shared
-// expert is e4m3 with fp32 128x128 block scales, or bf16 likewise.
-enum Fmt : int { kFp4E8M0 = 0, kFp4F32 = 1, kFp8Block = 2, kBf16 = 3 };
-
-// A "step" is 128 consecutive columns of one weight row.  Lane (r, g) of a
-// wave owns columns 128*st + 32g .. +32 of row r: the 4 lanes of a row read
-// the step's bytes contiguously, and MFMA j of the step uses the lane's
-// columns +8j .. +8j+7 (so its k-slot 8g+jj is column 128*st + 32g + 8j + jj).
-// Batch<F, kB> holds the raw loads of kB consecutive steps; nothing is
-// decoded until every load of the batch has been issued.
-template <int F, int kB>
-struct Batch;
-
-template <int kB>
-struct Batch<kFp4E8M0, kB> {
-  uint4 a[kB];
-  uint4 sq[kB >= 4 ? kB / 4 : 1];  // kB >= 4: 16 scale bytes per 4 steps (bytes 4b..4b+3 = step b)
-  uint32_t sb[kB];                 // kB < 4: one scale byte per step
-  __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
-    const uint8_t* base = (const uint8_t*)w + row * (k / 2) + st * 64 + g * 16;
-#pragma unroll
-    for (int b = 0; b < kB; ++b) a[b] = *reinterpret_cast<const uint4*>(base + b * 64);
-    const uint8_t* sp = (const uint8_t*)sc + row * (k / 32) + st * 4;
-    if constexpr (kB >= 4) {
-#pragma unroll
-      for (int q = 0; q < kB / 4; ++q) sq[q] = *reinterpret_cast<const uint4*>(sp + 16 * q);
-    } else {
-#pragma unroll
-      for (int b = 0; b < kB; ++b) sb[b] = sp[4 * b + g];
-    }
-  }
-  __device__ __forceinline__ bf16x8 frag(int b, int j, int g) const {
-    const uint4& q = a[b];
-    const uint32_t dw = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
-    uint32_t e;
-    if constexpr (kB >= 4) {
-      const uint4& s4 = sq[b / 4];
-      const int d = b & 3;
-      const uint32_t word = d == 0 ? s4.x : d == 1 ? s4.y : d == 2 ? s4.z : s4.w;
-      e = (word >> (8 * g)) & 0xffu;
-    } else {
-      e = sb[b];
-    }
-    return fp4x8_to_bf16_e8m0(dw, e8m0_as_f32(e));
-  }
-};
-
-template <int kB>
-struct Batch<kFp4F32, kB> {
-  uint4 a[kB];
-  float s[kB];
-  __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
-    const uint8_t* base = (const uint8_t*)w + row * (k / 2) + st * 64 + g * 16;
-    const float* sp = (const float*)sc + row * (k / 32) + st * 4 + g;
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      a[b] = *reinterpret_cast<const uint4*>(base + b * 64);
-      s[b] = sp[4 * b];
-    }
-  }
-  __device__ __forceinline__ bf16x8 frag(int b, int j, int) const {
-    const uint4& q = a[b];
-    const uint32_t dw = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
-    return fp4x8_to_bf16_f32(dw, s[b]);
-  }
-};
-
-template <int kB>
-struct Batch<kFp8Block, kB> {
-  uint4 a[kB], c[kB];
-  float s[kB];
-  __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
-    const uint8_t* base = (const uint8_t*)w + row * k + st * 128 + g * 32;
-    const float* sp = (const float*)sc + (row / 128) * (k / 128) + st;
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      a[b] = *reinterpret_cast<const uint4*>(base + b * 128);
-      c[b] = *reinterpret_cast<const uint4*>(base + b * 128 + 16);
-      s[b] = sp[b];
-    }
-  }
-  __device__ __forceinline__ bf16x8 frag(int b, int j, int) const {
-    const uint4& q = j < 2 ? a[b] : c[b];
-    const uint32_t d0 = (j & 1) ? q.z : q.x, d1 = (j & 1) ? q.w : q.y;
-    bf16x8 f;
-    fp8x4_to_bf16(d0, s[b], f, 0);
-    fp8x4_to_bf16(d1, s[b], f, 1);
-    return f;
-  }
-};
-
-template <int kB>
-struct Batch<kBf16, kB> {
-  uint4 a[kB][4];
-  __device__ __forceinline__ void load(uint64_t w, uint64_t, int64_t row, int64_t k, int64_t st, int g) {
-    const uint4* base = reinterpret_cast<const uint4*>((const uint16_t*)w + row * k + st * 128 + g * 32);
-#pragma unroll
-    for (int b = 0; b < kB; ++b)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) a[b][j] = base[b * 16 + j];
-  }
-  __device__ __forceinline__ bf16x8 frag(int b, int j, int) const { return __builtin_bit_cast(bf16x8, a[b][j]); }
-};
-
-// Steps per batch (register budget: ~64 VGPRs of raw weights per matrix).
-template <int F>
-constexpr int max_batch() {
-  return (F == kFp4E8M0 || F == kFp4F32) ? 8 : (F == kFp8Block ? 4 : 2);
-}
-
-__device__ __forceinline__ int slot_format(const DecodeParams& p, const uint64_t* ent, bool is_shared) {
-  if (is_shared) return ent[1] ? kFp8Block : kBf16;
-  return ent[1] ? p.scale_fmt : kBf16;
-}
-
-// B operand from an LDS tile laid out [16 columns][kcols] bf16: lane (c, g)
-// takes columns 128*st + 32g + 8j .. +8 of tile column c (zero when c >= ncol).
-__device__ __forceinline__ bf16x8 lds_frag(const uint16_t* tile, int kcols, int c, int g, int st, int j, int ncol) {
-  bf16x8 z = {};
-  if (c >= ncol) return z;
-  return *reinterpret_cast<const bf16x8*>(tile + c * kcols + st * 128 + g * 32 + 8 * j);
-}
-
-// ---------------------------------------------------------------- phase 1
-// Wave w of the block streams rows r0..r0+15 of W1 and W3 over its quarter of
-// the d/128 steps; x [m][d] sits in LDS.
-template <int F, int kB>
-__device__ __forceinline__ void gate_up(const DecodeParams& p, const uint64_t* ent, const uint16_t* xs, int r0,
-                                        int st0, int st1, f32x4& ag, f32x4& au) {
-  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  const int64_t row = r0 + r;
-  for (int st = st0; st < st1; st += kB) {
-    Batch<F, kB> b1, b3;
-    b1.load(ent[0], ent[1], row, p.d, st, g);
-    b3.load(ent[2], ent[3], row, p.d, st, g);
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bf16x8 xf = lds_frag(xs, p.d, r, g, st + b, j, p.m);
-        ag = mfma16x16x32(b1.frag(b, j, g), xf, ag);
-        au = mfma16x16x32(b3.frag(b, j, g), xf, au);
-      }
-    }
-  }
-}
-
-template <int F>
-__device__ __forceinline__ void gate_up_dispatch(const DecodeParams& p, const uint64_t* ent, const uint16_t* xs,
-                                                 int r0, int st0, int st1, f32x4& ag, f32x4& au) {
-  const int n = st1 - st0;
-  constexpr int kMax = max_batch<F>();
-  if (n % kMax == 0) gate_up<F, kMax>(p, ent, xs, r0, st0, st1, ag, au);
-  else if (kMax > 4 && n % 4 == 0) gate_up<F, (kMax > 4 ? 4 : 1)>(p, ent, xs, r0, st0, st1, ag, au);
-  else if (kMax > 2 && n % 2 == 0) gate_up<F, (kMax > 2 ? 2 : 1)>(p, ent, xs, r0, st0, st1, ag, au);
-  else gate_up<F, 1>(p, ent, xs, r0, st0, st1, ag, au);
-}
-
 __global__ void __launch_bounds__(64 * kP1Waves) moe_gate_up_kernel(DecodeParams p) {
   extern __shared__ __align__(16) uint16_t xs[];  // [m][d] bf16
   __shared__ Plan plan;
@@ -280,12 +121,7 @@ __global__ void __launch_bounds__(64 * kP1Waves) moe_gate_up_kernel(DecodeParams
   const int per = (p.d / 128) / kP1Waves;
   const int st0 = wave * per, st1 = st0 + per;
   f32x4 ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
-  switch (slot_format(p, ent, is_shared)) {
-    case kFp4E8M0: gate_up_dispatch<kFp4E8M0>(p, ent, xs, r0, st0, st1, ag, au); break;
-    case kFp4F32: gate_up_dispatch<kFp4F32>(p, ent, xs, r0, st0, st1, ag, au); break;
-    case kFp8Block: gate_up_dispatch<kFp8Block>(p, ent, xs, r0, st0, st1, ag, au); break;
-    default: gate_up_dispatch<kBf16>(p, ent, xs, r0, st0, st1, ag, au); break;
-  }
+  gate_up_slot(slot_format(p.scale_fmt, ent, is_shared), ent, xs, p.m, p.d, r0, st0, st1, ag, au);
   // D[4*(lane/16) + q][lane%16] lives in element q of lane
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -302,11 +138,7 @@ __global__ void __launch_bounds__(64 * kP1Waves) moe_gate_up_kernel(DecodeParams
       gsum = __fadd_rn(gsum, red[w][0][threadIdx.x]);
       usum = __fadd_rn(usum, red[w][1][threadIdx.x]);
     }
-    const float L = p.limit;
-    const float gc = gsum > L ? L : gsum;                          // clamp(max=L), NaN passes
-    const float uc = usum < -L ? -L : (usum > L ? L : usum);       // clamp(-L, L)
-    const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gc)));  // torch sigmoid
-    const float act = __fmul_rn(__fmul_rn(gc, sig), uc);
+    const float act = swiglu(gsum, usum, p.limit);
     const float a = __fmul_rn(s_wt[col], act);
     const uint32_t hi = f32_to_bf16_bits(a);
     const uint32_t lo = f32_to_bf16_bits(__fadd_rn(a, -bf16_bits_to_f32(hi)));
@@ -324,34 +156,6 @@ __global__ void __launch_bounds__(64 * kP1Waves) moe_gate_up_kernel(DecodeParams
 // finish (atomic arrival count) adds the slots' partials in slot order and
 // writes the output, then re-arms the counter: deterministic, and nothing
 // ever waits on another block.
-template <int F, int kB>
-__device__ __forceinline__ void down_rows(const DecodeParams& p, const uint64_t* ent, const uint16_t* as, int r0,
-                                          f32x4& acc) {
-  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  const int64_t row = r0 + r;
-  const int n = p.i / 128;
-  for (int st = 0; st < n; st += kB) {
-    Batch<F, kB> bw;
-    bw.load(ent[4], ent[5], row, p.i, st, g);
-#pragma unroll
-    for (int b = 0; b < kB; ++b)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc = mfma16x16x32(bw.frag(b, j, g), lds_frag(as, p.i, r, g, st + b, j, 2 * p.m), acc);
-  }
-}
-
-template <int F>
-__device__ __forceinline__ void down_dispatch(const DecodeParams& p, const uint64_t* ent, const uint16_t* as, int r0,
-                                              f32x4& acc) {
-  const int n = p.i / 128;
-  constexpr int kMax = (F == kFp4E8M0 || F == kFp4F32) ? 16 : max_batch<F>();
-  if (n % kMax == 0) down_rows<F, kMax>(p, ent, as, r0, acc);
-  else if (kMax > 8 && n % 8 == 0) down_rows<F, (kMax > 8 ? 8 : 1)>(p, ent, as, r0, acc);
-  else if (kMax > 4 && n % 4 == 0) down_rows<F, (kMax > 4 ? 4 : 1)>(p, ent, as, r0, acc);
-  else if (kMax > 2 && n % 2 == 0) down_rows<F, (kMax > 2 ? 2 : 1)>(p, ent, as, r0, acc);
-  else down_rows<F, 1>(p, ent, as, r0, acc);
-}
-
 __global__ void __launch_bounds__(64 * kP2Waves) moe_down_kernel(DecodeParams p) {
   extern __shared__ __align__(16) uint16_t as[];  // [2m][i] bf16
   __shared__ Plan plan;
@@ -361,6 +165,20 @@ __global__ void __launch_bounds__(64 * kP2Waves) moe_down_kernel(DecodeParams p)
   build_plan(p, plan, s_cand, s_first);
   const int n_slots = plan.n_routed + (p.shared ? 1 : 0);
   const int s = blockIdx.y;
+  if (n_slots == 0) {
+    // no valid expert and no shared expert: the output is zero
+    // (_forward_legacy returns zeros_like, fused_moe.py:473-474, 512-513)
+    if (s == 0) {
+      const int rows = 16 * kP2Waves;
+      for (int q = threadIdx.x; q < rows * p.m; q += blockDim.x) {
+        const int t = q / rows;
+        const int64_t o = (int64_t)t * p.d + blockIdx.x * rows + (q - t * rows);
+        if (p.out_f32) p.out_f32[o] = 0.0f;
+        if (p.out_bf16) p.out_bf16[o] = 0;
+      }
+    }
+    return;
+  }
   if (s >= n_slots) return;  // not counted: the arrival target is n_slots
   const bool is_shared = s == plan.n_routed;
   const uint64_t* ent = is_shared ? p.shared : p.table + (int64_t)plan.eid[s] * 6;
@@ -368,15 +186,13 @@ __global__ void __launch_bounds__(64 * kP2Waves) moe_down_kernel(DecodeParams p)
   const int r0 = blockIdx.x * (16 * kP2Waves) + 16 * wave;
   const int n16 = 2 * p.m * p.i / 8;
   const uint4* src = reinterpret_cast<const uint4*>(p.act + (int64_t)s * 2 * p.m * p.i);
-  for (int q = threadIdx.x; q < n16; q += blockDim.x) reinterpret_cast<uint4*>(as)[q] = src[q];
-  __syncthreads();
   f32x4 acc = {0, 0, 0, 0};
-  switch (slot_format(p, ent, is_shared)) {
-    case kFp4E8M0: down_dispatch<kFp4E8M0>(p, ent, as, r0, acc); break;
-    case kFp4F32: down_dispatch<kFp4F32>(p, ent, as, r0, acc); break;
-    case kFp8Block: down_dispatch<kFp8Block>(p, ent, as, r0, acc); break;
-    default: down_dispatch<kBf16>(p, ent, as, r0, acc); break;
-  }
+  // the W2 rows do not depend on the activations: their first batch is in
+  // flight while the tile is staged
+  down_slot(slot_format(p.scale_fmt, ent, is_shared), ent, as, p.m, p.i, r0, acc, [&]() {
+    for (int q = threadIdx.x; q < n16; q += blockDim.x) reinterpret_cast<uint4*>(as)[q] = src[q];
+    __syncthreads();
+  });
   // lane (col = lane%16) holds rows 4*(lane/16)+q; column t (hi) + column m+t (lo)
   // of token t are combined through the lane that owns column t.
   // Cross-block handoff without cache flushes: partials are written with

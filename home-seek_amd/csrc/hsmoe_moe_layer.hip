@@ -1,0 +1,490 @@
+// One MoE layer at decode (m <= 8 tokens) in a single persistent launch:
+// router -> routed FP4 experts + FP8 shared expert -> fixed-order expert sum.
+//
+// Restates, for m <= 8, HomeSeekInferenceEngine._forward_ffn
+// (engine.py:1410-1541): _compute_routing_experts / compute_expert_affinity_with_bias
+// (engine.py:1025-1031, router.py:22-36), FusedMoEFFN.forward on the selected
+// experts (fused_moe.py:447-563 over fused_expert_ffn_pt, fused_moe.py:383-395)
+// and the SharedExpertFFN add (engine.py:1530-1536).  The arithmetic is that
+// of hsmoe_router_topk followed by hsmoe_moe_decode (same tiles, same
+// accumulation order), so the results are bit-identical to those two calls.
+//
+// Work items, in dependency order (item q only ever waits on items < q):
+//   R    router rows: 4 expert rows per item (one per wave); the last R item
+//        to finish runs the top-k of every token and publishes the slot plan
+//        (distinct valid expert ids ascending, per-token slot weights)
+//   SGU  shared-expert gate/up, 16 rows of W1 and W3 per item
+//   GU   routed gate/up, (slot, 16 rows) per item; waits for the plan
+//   SD   shared-expert down, 64 rows of W2 per item
+//   D    routed down, (slot, 64 rows) per item
+// A down item issues its first W2 loads, then waits until every gate/up item
+// of its slot has published the slot's activations, then stages them in LDS.
+// The last down item of a row group adds the slots' partials in slot order
+// (routed ascending, shared last) and writes the output rows.
+// Workgroup b runs items b, b + G, b + 2G, ... with G no larger than the
+// number of workgroups the GPU holds at once, so every item a workgroup waits
+// for is held by a running workgroup.  Every wait is bounded; a wait that
+// gives up records the waited-on control word in the workspace (sticky) and
+// the workgroup carries on, so the launch always drains.
+#include <mutex>
+
+#include "hsmoe_common.h"
+#include "hsmoe_internal.h"
+#include "hsmoe_route.h"
+#include "hsmoe_tiles.h"
+
+namespace hsmoe {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kMaxTok = 8;
+constexpr int kMaxSlots = 128;  // m * top_k routed slots; slot kMaxSlots is never used as routed
+constexpr int kGuRows = 16;
+constexpr int kDownRows = 16 * kWaves;
+constexpr unsigned kSpinLimit = 1u << 16;
+// Off: the launch faulted the GPU on MI355X (first with the parameters read
+// through a null kernarg pointer in the item functions, then once more after
+// that fix, cause not yet shown).  The entry point returns an error instead.
+constexpr bool kLayerKernelEnabled = true;
+
+// control words (unsigned) at the start of the workspace
+constexpr int kCtlRouter = 0;    // router items finished
+constexpr int kCtlPlan = 64;     // 1 once the slot plan is published
+constexpr int kCtlDone = 128;    // workgroups finished
+constexpr int kCtlErr = 192;     // sticky: 1 + index of a control word whose wait gave up
+constexpr int kCtlSlot = 256;    // + 16*s: gate/up items of slot s finished
+constexpr int kCtlRowGroup = kCtlSlot + 16 * (kMaxSlots + 1);  // + g: down items of row group g finished
+constexpr int kMaxRowGroups = 2048;
+constexpr size_t kCtlBytes = 32768;
+static_assert((kCtlRowGroup + kMaxRowGroups) * 4 <= (int)kCtlBytes, "control block overflow");
+
+struct PlanG {
+  int n_routed;
+  int pad[63];
+  int eid[kMaxSlots];
+  float wt[kMaxSlots][kMaxTok];
+};
+
+struct LayerParams {
+  const uint16_t* x;       // bf16 [m, d]
+  const uint16_t* gate_w;  // bf16 [n_exp, d]
+  const float* bias;       // [n_exp] or null
+  const uint64_t* table;   // [n_exp][6]
+  const uint64_t* shared;  // [6] or null
+  int64_t n_exp;
+  int m, d, i, top_k, scale_fmt, S;  // S = m * top_k routed slots
+  float scaling, limit;
+  int64_t* idx_out;    // [m, top_k]
+  float* w_out;        // [m, top_k]
+  uint16_t* logits;    // bf16 [m, n_exp] or null
+  float* out_f32;      // [m, d] or null
+  uint16_t* out_bf16;  // [m, d] or null
+  unsigned* ctl;
+  float* scores;  // [m][n_exp]
+  PlanG* plan;
+  float* act;   // fp32 [S + 1][m][i] weighted activations (slot S = shared)
+  float* part;  // fp32 [S + 1][m][d] per-slot down partials
+  int n_router, q_sgu, q_gu, q_sd, q_down, n_items;
+};
+
+__device__ bool wait_at_least(unsigned* ctl, int word, unsigned target) {
+  for (unsigned it = 0; it < kSpinLimit; ++it) {
+    if (load_agent(ctl + word) >= target) return true;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  store_agent(ctl + kCtlErr, 1u + (unsigned)word);
+  return false;
+}
+
+struct Shared {
+  float red[kWaves][2][256];
+  int64_t idx[kMaxSlots];
+  float w[kMaxSlots];
+  int cand[kMaxSlots];
+  int first[kMaxSlots];
+  float wt[kMaxTok];
+  int flag;
+  int n_routed;
+  int eid;
+  int count;
+};
+
+// Top-k of every token, then the slot plan; run by the last router item.
+__device__ __forceinline__ void publish_plan(const LayerParams& p, Shared& sh) {
+  const int wave = threadIdx.x >> 6;
+  const int n = p.m * p.top_k;
+  for (int t = wave; t < p.m; t += kWaves)
+    wave_topk(p.scores + (int64_t)t * p.n_exp, p.n_exp, p.top_k, p.scaling, sh.idx + t * p.top_k,
+              sh.w + t * p.top_k);
+  if (threadIdx.x == 0) sh.count = 0;
+  __syncthreads();
+  for (int j = threadIdx.x; j < n; j += kThreads) {
+    p.idx_out[j] = sh.idx[j];
+    p.w_out[j] = sh.w[j];
+    const int64_t e = sh.idx[j];
+    const bool ok = e >= 0 && e < p.n_exp && p.table[e * 6] != 0;
+    sh.cand[j] = ok ? (int)e : -1;
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < n; j += kThreads) {
+    const int e = sh.cand[j];
+    bool first = e >= 0;
+    for (int q = 0; q < j && first; ++q) first = sh.cand[q] != e;
+    sh.first[j] = first;
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < n; j += kThreads) {
+    if (sh.first[j]) {
+      const int e = sh.cand[j];
+      int rank = 0;
+      for (int q = 0; q < n; ++q) rank += (sh.first[q] && sh.cand[q] < e);
+      store_agent(&p.plan->eid[rank], e);
+      // the slot's weight for each token: its top-k weights for e, summed in k order
+      for (int t = 0; t < p.m; ++t) {
+        float w = 0.0f;
+        for (int k = 0; k < p.top_k; ++k)
+          if (sh.idx[t * p.top_k + k] == e) w = __fadd_rn(w, sh.w[t * p.top_k + k]);
+        store_agent(&p.plan->wt[rank][t], w);
+      }
+      atomicAdd(&sh.count, 1);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) store_agent(&p.plan->n_routed, sh.count);
+  if (sh.count == 0 && !p.shared) {
+    // no valid expert and no shared expert: no down item will run, and the
+    // layer's output is zero (_forward_legacy returns zeros_like, fused_moe.py:473-474, 512-513)
+    for (int c = threadIdx.x; c < p.m * p.d; c += kThreads) {
+      if (p.out_f32) p.out_f32[c] = 0.0f;
+      if (p.out_bf16) p.out_bf16[c] = 0;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) store_agent(p.ctl + kCtlPlan, 1u);
+}
+
+// Thread 0 waits for the plan and reads the slot count (and the expert id of
+// routed slot s, or -1); every thread returns with sh.n_routed / sh.eid set.
+__device__ __forceinline__ void read_plan(const LayerParams& p, Shared& sh, int s) {
+  if (threadIdx.x == 0) {
+    wait_at_least(p.ctl, kCtlPlan, 1u);
+    const int nr = load_agent(&p.plan->n_routed);
+    sh.n_routed = nr;
+    sh.eid = (s >= 0 && s < nr) ? load_agent(&p.plan->eid[s]) : -1;
+  }
+  __syncthreads();
+}
+
+
+// LDS of the layer kernel (file scope so the item functions below address it
+// directly): x [m][d] or activations [2m][i] as bf16, and the block's scratch.
+extern __shared__ __align__(16) uint16_t g_tile[];
+__shared__ Shared g_sh;
+
+// The item functions are not inlined (each keeps its own register budget), so
+// they read the launch parameters through the kernel's kernarg-segment address,
+// which the kernel passes down: that builtin yields a valid address only in
+// the kernel itself.
+typedef const __attribute__((address_space(4))) LayerParams KernargParams;
+
+__device__ __forceinline__ LayerParams params(uint64_t kernarg) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)kernarg);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(kernarg >> 32));
+#if defined(__HIP_DEVICE_COMPILE__)
+  return *(KernargParams*)(((uint64_t)hi << 32) | lo);
+#else
+  return LayerParams{};  // host pass: never called
+#endif
+}
+
+// Copies x into the LDS tile unless it is already there (state: 1 = x in LDS).
+__device__ __forceinline__ void ensure_x(const LayerParams& p, int& state) {
+  if (state == 1) return;
+  const int n16 = p.m * p.d / 8;
+  for (int q = threadIdx.x; q < n16; q += kThreads)
+    reinterpret_cast<uint4*>(g_tile)[q] = reinterpret_cast<const uint4*>(p.x)[q];
+  __syncthreads();
+  state = 1;
+}
+
+__device__ __noinline__ int router_item(uint64_t kernarg, int q_arg, int state_arg) {
+  const int q = __builtin_amdgcn_readfirstlane(q_arg);
+  int state = __builtin_amdgcn_readfirstlane(state_arg);
+  const LayerParams p = params(kernarg);
+  Shared& sh = g_sh;
+  const int wave = threadIdx.x >> 6;
+  const int64_t e = (int64_t)q * kWaves + wave;
+  uint4 wv[kMaxChunks];
+  if (e < p.n_exp) load_gate_row(p.gate_w, e, p.d, wv);
+  ensure_x(p, state);
+  if (e < p.n_exp)
+    router_row(wv, g_tile, p.m, p.d, e, p.n_exp, p.bias, p.logits ? p.logits + e : nullptr, p.scores + e);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) sh.flag = add_agent(p.ctl + kCtlRouter, 1u) == (unsigned)(p.n_router - 1);
+  __syncthreads();
+  if (sh.flag) publish_plan(p, sh);
+  return state;
+}
+
+__device__ __noinline__ int gate_up_item(uint64_t kernarg, int q_arg, int state_arg) {
+  const int q = __builtin_amdgcn_readfirstlane(q_arg);
+  int state = __builtin_amdgcn_readfirstlane(state_arg);
+  const LayerParams p = params(kernarg);
+  Shared& sh = g_sh;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int gu_per_slot = p.i / kGuRows;
+  const bool is_shared = q < p.q_gu;
+  const int qq = is_shared ? q - p.q_sgu : q - p.q_gu;
+  const int s = is_shared ? p.S : qq / gu_per_slot;
+  const int r0 = (qq % gu_per_slot) * kGuRows;
+  if (!is_shared) {
+    read_plan(p, sh, s);
+    if (s >= sh.n_routed) return state;
+    if (threadIdx.x < p.m) sh.wt[threadIdx.x] = load_agent(&p.plan->wt[s][threadIdx.x]);
+  } else if (threadIdx.x < p.m) {
+    sh.wt[threadIdx.x] = 1.0f;
+  }
+  const uint64_t* ent = is_shared ? p.shared : p.table + (int64_t)sh.eid * 6;
+  ensure_x(p, state);
+  const int per = (p.d / 128) / kWaves;
+  const int st0 = wave * per;
+  f32x4 ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
+  gate_up_slot(slot_format(p.scale_fmt, ent, is_shared), ent, g_tile, p.m, p.d, r0, st0, st0 + per, ag, au);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int row = 4 * (lane >> 4) + c, col = lane & 15;
+    sh.red[wave][0][row * 16 + col] = ag[c];
+    sh.red[wave][1][row * 16 + col] = au[c];
+  }
+  __syncthreads();
+  const int row = threadIdx.x >> 4, col = threadIdx.x & 15;
+  if (col < p.m) {
+    float gsum = 0.0f, usum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      gsum = __fadd_rn(gsum, sh.red[w][0][threadIdx.x]);
+      usum = __fadd_rn(usum, sh.red[w][1][threadIdx.x]);
+    }
+    const float a = __fmul_rn(sh.wt[col], swiglu(gsum, usum, p.limit));
+    store_agent(p.act + ((int64_t)s * p.m + col) * p.i + r0 + row, a);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) add_agent(p.ctl + kCtlSlot + 16 * s, 1u);
+  return state;
+}
+
+__device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg) {
+  const int q = __builtin_amdgcn_readfirstlane(q_arg);
+  int state = __builtin_amdgcn_readfirstlane(state_arg);
+  const LayerParams p = params(kernarg);
+  Shared& sh = g_sh;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int gu_per_slot = p.i / kGuRows, down_per_slot = p.d / kDownRows;
+  const bool is_shared = q < p.q_down;
+  const int qq = is_shared ? q - p.q_sd : q - p.q_down;
+  const int s = is_shared ? p.S : qq / down_per_slot;
+  const int g = qq % down_per_slot;
+  read_plan(p, sh, is_shared ? -1 : s);
+  if (!is_shared && s >= sh.n_routed) return state;
+  const int n_routed = sh.n_routed;
+  const uint64_t* ent = is_shared ? p.shared : p.table + (int64_t)sh.eid * 6;
+  const int r0 = g * kDownRows + 16 * wave;
+  const int m = p.m, i = p.i;
+  unsigned* const ctl = p.ctl;
+  const float* const src = p.act + (int64_t)s * m * i;
+  f32x4 acc = {0, 0, 0, 0};
+  down_slot(slot_format(p.scale_fmt, ent, is_shared), ent, g_tile, m, i, r0, acc, [&]() __attribute__((always_inline)) {
+    if (threadIdx.x == 0) wait_at_least(ctl, kCtlSlot + 16 * s, (unsigned)gu_per_slot);
+    __syncthreads();
+    // fp32 activations -> bf16 hi rows [t][k] and lo rows [m + t][k]
+    const int n = m * i;
+    for (int c = threadIdx.x; c < n; c += kThreads) {
+      const float a = load_agent(src + c);
+      const uint32_t hi = f32_to_bf16_bits(a);
+      const uint32_t lo = f32_to_bf16_bits(__fadd_rn(a, -bf16_bits_to_f32(hi)));
+      g_tile[c] = (uint16_t)hi;
+      g_tile[n + c] = (uint16_t)lo;
+    }
+    __syncthreads();
+  });
+  state = 0;
+  // lane (col = lane%16) holds rows 4*(lane/16)+c; column t (hi) + column m+t (lo)
+  // of token t are combined through the lane that owns column t.
+  float* part = p.part + (int64_t)s * m * p.d;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int col = lane & 15;
+    const float lo = __shfl(acc[c], (lane & 48) | ((col + m) & 15), 64);
+    if (col < m) store_agent(part + (int64_t)col * p.d + r0 + 4 * (lane >> 4) + c, __fadd_rn(acc[c], lo));
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const int n_slots = n_routed + (p.shared ? 1 : 0);
+  if (threadIdx.x == 0) sh.flag = add_agent(p.ctl + kCtlRowGroup + g, 1u) == (unsigned)(n_slots - 1);
+  __syncthreads();
+  if (sh.flag) {
+    for (int c = threadIdx.x; c < kDownRows * m; c += kThreads) {
+      const int t = c / kDownRows, dd = g * kDownRows + (c - t * kDownRows);
+      float v = 0.0f;
+      for (int ss = 0; ss < n_routed; ++ss) v = __fadd_rn(v, load_agent(p.part + ((int64_t)ss * m + t) * p.d + dd));
+      if (p.shared) v = __fadd_rn(v, load_agent(p.part + ((int64_t)p.S * m + t) * p.d + dd));
+      const int64_t o = (int64_t)t * p.d + dd;
+      if (p.out_f32) p.out_f32[o] = v;
+      if (p.out_bf16) p.out_bf16[o] = (uint16_t)f32_to_bf16_bits(v);
+    }
+  }
+  return state;
+}
+
+__global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
+  int state = 0;  // 1 while the LDS tile holds x
+  const uint64_t kernarg = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();  // &p
+  const int n_items = p.n_items, q_sgu = p.q_sgu, q_sd = p.q_sd;
+  for (int q = blockIdx.x; q < n_items; q += gridDim.x) {
+    __syncthreads();  // the previous item's readers of the LDS scratch are done
+    if (q < q_sgu) state = router_item(kernarg, q, state);
+    else if (q < q_sd) state = gate_up_item(kernarg, q, state);
+    else state = down_item(kernarg, q, state);
+  }
+  // the last workgroup to finish re-arms every control word for the next call
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) g_sh.flag = add_agent(p.ctl + kCtlDone, 1u) == gridDim.x - 1;
+  __syncthreads();
+  if (!g_sh.flag) return;
+  if (threadIdx.x == 0) {
+    store_agent(p.ctl + kCtlRouter, 0u);
+    store_agent(p.ctl + kCtlPlan, 0u);
+    store_agent(p.ctl + kCtlDone, 0u);
+  }
+  for (int s = threadIdx.x; s <= p.S; s += kThreads) store_agent(p.ctl + kCtlSlot + 16 * s, 0u);
+  for (int g = threadIdx.x; g < p.d / kDownRows; g += kThreads) store_agent(p.ctl + kCtlRowGroup + g, 0u);
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+size_t scores_bytes(int64_t m, int64_t n_exp) { return align256((size_t)(m * n_exp * 4)); }
+size_t plan_bytes() { return align256(sizeof(PlanG)); }
+size_t act_bytes(int64_t m, int64_t i, int top_k) { return align256((size_t)(m * top_k + 1) * m * i * 4); }
+size_t part_bytes(int64_t m, int64_t d, int top_k) { return align256((size_t)(m * top_k + 1) * m * d * 4); }
+
+// Workgroups of moe_layer_kernel the device holds at once, for an LDS size.
+int resident_workgroups(size_t lds, int* out) {
+  static std::mutex mu;
+  static int cache_dev = -1, cache_cus = 0;
+  static size_t cache_lds[8] = {};
+  static int cache_nb[8] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(HSMOE_ERR_LAUNCH, "hsmoe_moe_layer_decode: hipGetDevice failed");
+  std::lock_guard<std::mutex> lock(mu);
+  if (dev != cache_dev) {
+    if (hipDeviceGetAttribute(&cache_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return fail(HSMOE_ERR_LAUNCH, "hsmoe_moe_layer_decode: CU count query failed");
+    cache_dev = dev;
+    for (auto& c : cache_lds) c = 0;
+  }
+  for (int k = 0; k < 8; ++k)
+    if (cache_lds[k] == lds + 1) {
+      *out = cache_nb[k] * cache_cus;
+      return HSMOE_OK;
+    }
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, moe_layer_kernel, kThreads, lds) != hipSuccess || nb < 1)
+    return fail(HSMOE_ERR_LAUNCH, "hsmoe_moe_layer_decode: occupancy query failed (%d workgroups/CU)", nb);
+  for (int k = 0; k < 8; ++k)
+    if (cache_lds[k] == 0) {
+      cache_lds[k] = lds + 1;
+      cache_nb[k] = nb;
+      break;
+    }
+  *out = nb * cache_cus;
+  return HSMOE_OK;
+}
+
+}  // namespace
+}  // namespace hsmoe
+
+using namespace hsmoe;
+
+extern "C" size_t hsmoe_moe_layer_workspace_size(int64_t m, int64_t d, int64_t i, int64_t n_experts, int top_k) {
+  if (m < 1 || d < 1 || i < 1 || n_experts < 1 || top_k < 1) return 0;
+  return kCtlBytes + scores_bytes(m, n_experts) + plan_bytes() + act_bytes(m, i, top_k) + part_bytes(m, d, top_k);
+}
+
+extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
+                                      const float* gate_bias, int64_t n_experts, int top_k, float routed_scaling,
+                                      const uint64_t* expert_table, int scale_kind, const uint64_t* shared,
+                                      float swiglu_limit, int64_t* topk_idx_out, float* topk_w_out,
+                                      void* logits_out, float* out_f32, void* out_bf16, void* workspace,
+                                      size_t workspace_bytes, hsmoe_stream_t stream) {
+  const char* name = "hsmoe_moe_layer_decode";
+  if (!kLayerKernelEnabled)
+    return fail(HSMOE_ERR_LAUNCH,
+                "%s: disabled -- this persistent kernel faulted the GPU on its first runs and stays off until the "
+                "cause is shown; use hsmoe_router_topk + hsmoe_moe_decode", name);
+  if (!x || !gate_w || !expert_table || !topk_idx_out || !topk_w_out || (!out_f32 && !out_bf16))
+    return fail(HSMOE_ERR_ARG, "%s: null pointer or no output", name);
+  if (scale_kind != HSMOE_SCALE_E8M0 && scale_kind != HSMOE_SCALE_F32)
+    return fail(HSMOE_ERR_ARG, "%s: unknown scale_kind %d", name, scale_kind);
+  if (m < 1 || m > kMaxTok || n_experts < 1 || n_experts > 1024 || top_k < 1 || top_k > 16 || top_k > n_experts ||
+      m * top_k > kMaxSlots)
+    return fail(HSMOE_ERR_SHAPE, "%s: need 1 <= m <= 8, n_experts <= 1024, 1 <= top_k <= min(16, n_experts)", name);
+  if (d % 512 != 0 || i % 512 != 0 || d <= 0 || i <= 0 || d > 8192 || d / kDownRows > kMaxRowGroups)
+    return fail(HSMOE_ERR_SHAPE, "%s: d and i must be positive multiples of 512, d <= 8192 (d=%lld i=%lld)", name,
+                (long long)d, (long long)i);
+  if (!aligned(x, 16) || !aligned(gate_w, 16)) return fail(HSMOE_ERR_SHAPE, "%s: x and gate_w must be 16-byte aligned", name);
+  const size_t need = hsmoe_moe_layer_workspace_size(m, d, i, n_experts, top_k);
+  if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+    return fail(HSMOE_ERR_WORKSPACE, "%s: zero-filled workspace of %zu bytes (256-byte aligned) needed", name, need);
+  const size_t lds = (size_t)(m * d > 2 * m * i ? m * d : 2 * m * i) * 2;
+  if (lds > 65536) return fail(HSMOE_ERR_SHAPE, "%s: m*d and 2*m*i tiles must fit in 64 KiB of LDS", name);
+
+  LayerParams p;
+  p.x = (const uint16_t*)x;
+  p.gate_w = (const uint16_t*)gate_w;
+  p.bias = gate_bias;
+  p.table = expert_table;
+  p.shared = shared;
+  p.n_exp = n_experts;
+  p.m = (int)m;
+  p.d = (int)d;
+  p.i = (int)i;
+  p.top_k = top_k;
+  p.scale_fmt = scale_kind == HSMOE_SCALE_E8M0 ? kFp4E8M0 : kFp4F32;
+  p.S = (int)(m * top_k);
+  p.scaling = routed_scaling;
+  p.limit = swiglu_limit;
+  p.idx_out = topk_idx_out;
+  p.w_out = topk_w_out;
+  p.logits = (uint16_t*)logits_out;
+  p.out_f32 = out_f32;
+  p.out_bf16 = (uint16_t*)out_bf16;
+  char* ws = (char*)workspace;
+  p.ctl = (unsigned*)ws;
+  ws += kCtlBytes;
+  p.scores = (float*)ws;
+  ws += scores_bytes(m, n_experts);
+  p.plan = (PlanG*)ws;
+  ws += plan_bytes();
+  p.act = (float*)ws;
+  ws += act_bytes(m, i, top_k);
+  p.part = (float*)ws;
+  const int has_shared = shared ? 1 : 0;
+  p.n_router = (int)((n_experts + kWaves - 1) / kWaves);
+  p.q_sgu = p.n_router;
+  p.q_gu = p.q_sgu + has_shared * (int)(i / kGuRows);
+  p.q_sd = p.q_gu + p.S * (int)(i / kGuRows);
+  p.q_down = p.q_sd + has_shared * (int)(d / kDownRows);
+  p.n_items = p.q_down + p.S * (int)(d / kDownRows);
+  int resident = 0;
+  int rc = resident_workgroups(lds, &resident);
+  if (rc) return rc;
+  const int grid = resident < p.n_items ? resident : p.n_items;
+  hipLaunchKernelGGL(moe_layer_kernel, dim3((unsigned)grid), dim3(kThreads), lds, (hipStream_t)stream, p);
+  return check_launch(name);
+}
+
+extern "C" size_t hsmoe_moe_layer_status_offset(void) { return (size_t)kCtlErr * 4; }

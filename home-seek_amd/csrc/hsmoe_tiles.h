@@ -1,0 +1,274 @@
+// Weight-streaming tiles shared by the decode kernels (stage kernels of
+// hsmoe_moe_decode and the fused layer kernel of hsmoe_moe_layer_decode).
+//
+// A "step" is 128 consecutive columns of one weight row.  Lane (r, g) of a
+// wave owns columns 128*st + 32g .. +32 of row r: the 4 lanes of a row read the
+// step's bytes contiguously, and MFMA j of the step uses the lane's columns
+// +8j .. +8j+7 (so its k-slot 8g+jj is column 128*st + 32g + 8j + jj).
+// Batch<F, kB> holds the raw loads of kB consecutive steps; nothing is decoded
+// until every load of the batch has been issued.
+//
+// Weight formats of a slot: routed experts are FP4 (e2m1) with E8M0 or fp32
+// per-32 scales, or bf16 when the table entry has no scale pointer; the shared
+// expert is e4m3 with fp32 128x128 block scales, or bf16 likewise.
+#pragma once
+#include "hsmoe_common.h"
+
+namespace hsmoe {
+
+enum Fmt : int { kFp4E8M0 = 0, kFp4F32 = 1, kFp8Block = 2, kBf16 = 3 };
+
+template <int F, int kB>
+struct Batch;
+
+template <int kB>
+struct Batch<kFp4E8M0, kB> {
+  uint4 a[kB];
+  uint4 sq[kB >= 4 ? kB / 4 : 1];  // kB >= 4: 16 scale bytes per 4 steps (bytes 4b..4b+3 = step b)
+  uint32_t sb[kB];                 // kB < 4: one scale byte per step
+  __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
+    const uint8_t* base = (const uint8_t*)w + row * (k / 2) + st * 64 + g * 16;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) a[b] = *reinterpret_cast<const uint4*>(base + b * 64);
+    const uint8_t* sp = (const uint8_t*)sc + row * (k / 32) + st * 4;
+    if constexpr (kB >= 4) {
+#pragma unroll
+      for (int q = 0; q < kB / 4; ++q) sq[q] = *reinterpret_cast<const uint4*>(sp + 16 * q);
+    } else {
+#pragma unroll
+      for (int b = 0; b < kB; ++b) sb[b] = sp[4 * b + g];
+    }
+  }
+  __device__ __forceinline__ bf16x8 frag(int b, int j, int g) const {
+    const uint4& q = a[b];
+    const uint32_t dw = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
+    uint32_t e;
+    if constexpr (kB >= 4) {
+      const uint4& s4 = sq[b / 4];
+      const int d = b & 3;
+      const uint32_t word = d == 0 ? s4.x : d == 1 ? s4.y : d == 2 ? s4.z : s4.w;
+      e = (word >> (8 * g)) & 0xffu;
+    } else {
+      e = sb[b];
+    }
+    return fp4x8_to_bf16_e8m0(dw, e8m0_as_f32(e));
+  }
+};
+
+template <int kB>
+struct Batch<kFp4F32, kB> {
+  uint4 a[kB];
+  float s[kB];
+  __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
+    const uint8_t* base = (const uint8_t*)w + row * (k / 2) + st * 64 + g * 16;
+    const float* sp = (const float*)sc + row * (k / 32) + st * 4 + g;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      a[b] = *reinterpret_cast<const uint4*>(base + b * 64);
+      s[b] = sp[4 * b];
+    }
+  }
+  __device__ __forceinline__ bf16x8 frag(int b, int j, int) const {
+    const uint4& q = a[b];
+    const uint32_t dw = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
+    return fp4x8_to_bf16_f32(dw, s[b]);
+  }
+};
+
+template <int kB>
+struct Batch<kFp8Block, kB> {
+  uint4 a[kB], c[kB];
+  float s[kB];
+  __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
+    const uint8_t* base = (const uint8_t*)w + row * k + st * 128 + g * 32;
+    const float* sp = (const float*)sc + (row / 128) * (k / 128) + st;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      a[b] = *reinterpret_cast<const uint4*>(base + b * 128);
+      c[b] = *reinterpret_cast<const uint4*>(base + b * 128 + 16);
+      s[b] = sp[b];
+    }
+  }
+  __device__ __forceinline__ bf16x8 frag(int b, int j, int) const {
+    const uint4& q = j < 2 ? a[b] : c[b];
+    const uint32_t d0 = (j & 1) ? q.z : q.x, d1 = (j & 1) ? q.w : q.y;
+    bf16x8 f;
+    fp8x4_to_bf16(d0, s[b], f, 0);
+    fp8x4_to_bf16(d1, s[b], f, 1);
+    return f;
+  }
+};
+
+template <int kB>
+struct Batch<kBf16, kB> {
+  uint4 a[kB][4];
+  __device__ __forceinline__ void load(uint64_t w, uint64_t, int64_t row, int64_t k, int64_t st, int g) {
+    const uint4* base = reinterpret_cast<const uint4*>((const uint16_t*)w + row * k + st * 128 + g * 32);
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[b][j] = base[b * 16 + j];
+  }
+  __device__ __forceinline__ bf16x8 frag(int b, int j, int) const { return __builtin_bit_cast(bf16x8, a[b][j]); }
+};
+
+// Steps per batch of the gate/up streams (register budget: ~64 VGPRs of raw
+// weights per matrix) and of the down stream (one matrix, twice the steps).
+template <int F>
+constexpr int gate_up_batch() {
+  return (F == kFp4E8M0 || F == kFp4F32) ? 8 : (F == kFp8Block ? 4 : 2);
+}
+template <int F>
+constexpr int down_batch() {
+  return (F == kFp4E8M0 || F == kFp4F32) ? 16 : gate_up_batch<F>();
+}
+
+// Largest batch size <= kMax (a power of two) that divides n.
+template <int kMax>
+__device__ __forceinline__ int batch_for(int n) {
+  int b = kMax;
+  while (b > 1 && n % b != 0) b >>= 1;
+  return b;
+}
+
+// Format of the slot whose table entry is `ent`.
+__device__ __forceinline__ int slot_format(int routed_scale_fmt, const uint64_t* ent, bool is_shared) {
+  if (is_shared) return ent[1] ? kFp8Block : kBf16;
+  return ent[1] ? routed_scale_fmt : kBf16;
+}
+
+// B operand from an LDS tile laid out [16 columns][kcols] bf16: lane (c, g)
+// takes columns 128*st + 32g + 8j .. +8 of tile column c (zero when c >= ncol).
+__device__ __forceinline__ bf16x8 lds_frag(const uint16_t* tile, int kcols, int c, int g, int st, int j, int ncol) {
+  bf16x8 z = {};
+  if (c >= ncol) return z;
+  return *reinterpret_cast<const bf16x8*>(tile + c * kcols + st * 128 + g * 32 + 8 * j);
+}
+
+// ------------------------------------------------------------ gate / up
+// One wave: rows r0..r0+15 of W1 and W3 of the slot `ent` over steps
+// [st0, st1) against the m token rows of x ([m][d] bf16 in LDS).  The MFMA
+// accumulators hold D[4*(lane/16) + q][lane%16] = row r0 + 4*(lane/16) + q,
+// token lane%16.
+template <int F, int kB>
+__device__ __forceinline__ void gate_up_rows(const uint64_t* ent, const uint16_t* xs, int m, int d, int r0, int st0,
+                                             int st1, f32x4& ag, f32x4& au) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int64_t row = r0 + r;
+  for (int st = st0; st < st1; st += kB) {
+    Batch<F, kB> b1, b3;
+    b1.load(ent[0], ent[1], row, d, st, g);
+    b3.load(ent[2], ent[3], row, d, st, g);
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bf16x8 xf = lds_frag(xs, d, r, g, st + b, j, m);
+        ag = mfma16x16x32(b1.frag(b, j, g), xf, ag);
+        au = mfma16x16x32(b3.frag(b, j, g), xf, au);
+      }
+    }
+  }
+}
+
+template <int F>
+__device__ __forceinline__ void gate_up_any(const uint64_t* ent, const uint16_t* xs, int m, int d, int r0, int st0,
+                                            int st1, f32x4& ag, f32x4& au) {
+  constexpr int kMax = gate_up_batch<F>();
+  const int b = batch_for<kMax>(st1 - st0);
+  if (b == kMax) gate_up_rows<F, kMax>(ent, xs, m, d, r0, st0, st1, ag, au);
+  else if (kMax > 4 && b == 4) gate_up_rows<F, (kMax > 4 ? 4 : 1)>(ent, xs, m, d, r0, st0, st1, ag, au);
+  else if (kMax > 2 && b == 2) gate_up_rows<F, (kMax > 2 ? 2 : 1)>(ent, xs, m, d, r0, st0, st1, ag, au);
+  else gate_up_rows<F, 1>(ent, xs, m, d, r0, st0, st1, ag, au);
+}
+
+__device__ __forceinline__ void gate_up_slot(int fmt, const uint64_t* ent, const uint16_t* xs, int m, int d, int r0,
+                                             int st0, int st1, f32x4& ag, f32x4& au) {
+  switch (fmt) {
+    case kFp4E8M0: gate_up_any<kFp4E8M0>(ent, xs, m, d, r0, st0, st1, ag, au); break;
+    case kFp4F32: gate_up_any<kFp4F32>(ent, xs, m, d, r0, st0, st1, ag, au); break;
+    case kFp8Block: gate_up_any<kFp8Block>(ent, xs, m, d, r0, st0, st1, ag, au); break;
+    default: gate_up_any<kBf16>(ent, xs, m, d, r0, st0, st1, ag, au); break;
+  }
+}
+
+// SwiGLU of the reference's M<=8 route (fused_moe.py:390-395) in fp32:
+// min(g, L) * sigmoid(min(g, L)) * clamp(u, -L, L); NaN passes both clamps.
+__device__ __forceinline__ float swiglu(float gsum, float usum, float L) {
+  const float gc = gsum > L ? L : gsum;
+  const float uc = usum < -L ? -L : (usum > L ? L : usum);
+  const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gc)));  // torch sigmoid
+  return __fmul_rn(__fmul_rn(gc, sig), uc);
+}
+
+// ------------------------------------------------------------ down
+// One wave: rows r0..r0+15 of W2 of the slot `ent` over all i/128 steps
+// against the activation tile as ([2m][i] bf16 in LDS: hi rows then lo rows).
+// `ready()` runs (block-wide) after the first batch's loads are issued and
+// before the tile is read, so the weight loads overlap whatever it waits for.
+template <int F, int kB, typename Ready>
+__device__ __forceinline__ void down_rows(const uint64_t* ent, const uint16_t* as, int m, int i, int r0, f32x4& acc,
+                                          Ready&& ready) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int64_t row = r0 + r;
+  const int n = i / 128;
+  Batch<F, kB> bw;
+  bw.load(ent[4], ent[5], row, i, 0, g);
+  ready();
+  for (int st = 0; st < n; st += kB) {
+    if (st) bw.load(ent[4], ent[5], row, i, st, g);
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = mfma16x16x32(bw.frag(b, j, g), lds_frag(as, i, r, g, st + b, j, 2 * m), acc);
+  }
+}
+
+template <int F, typename Ready>
+__device__ __forceinline__ void down_any(const uint64_t* ent, const uint16_t* as, int m, int i, int r0, f32x4& acc,
+                                         Ready&& ready) {
+  constexpr int kMax = down_batch<F>();
+  const int b = batch_for<kMax>(i / 128);
+  if (b == kMax) down_rows<F, kMax>(ent, as, m, i, r0, acc, ready);
+  else if (kMax > 8 && b == 8) down_rows<F, (kMax > 8 ? 8 : 1)>(ent, as, m, i, r0, acc, ready);
+  else if (kMax > 4 && b == 4) down_rows<F, (kMax > 4 ? 4 : 1)>(ent, as, m, i, r0, acc, ready);
+  else if (kMax > 2 && b == 2) down_rows<F, (kMax > 2 ? 2 : 1)>(ent, as, m, i, r0, acc, ready);
+  else down_rows<F, 1>(ent, as, m, i, r0, acc, ready);
+}
+
+template <typename Ready>
+__device__ __forceinline__ void down_slot(int fmt, const uint64_t* ent, const uint16_t* as, int m, int i, int r0,
+                                          f32x4& acc, Ready&& ready) {
+  switch (fmt) {
+    case kFp4E8M0: down_any<kFp4E8M0>(ent, as, m, i, r0, acc, ready); break;
+    case kFp4F32: down_any<kFp4F32>(ent, as, m, i, r0, acc, ready); break;
+    case kFp8Block: down_any<kFp8Block>(ent, as, m, i, r0, acc, ready); break;
+    default: down_any<kBf16>(ent, as, m, i, r0, acc, ready); break;
+  }
+}
+
+// Agent-scope (cross-XCD coherent, L2-bypassing) loads and stores used for
+// every value one workgroup hands to another inside a launch.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int load_agent(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned load_agent(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned add_agent(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace hsmoe

@@ -14,7 +14,8 @@ from ._lib import SCALE_E8M0, SCALE_F32, check, lib, ptr, require_cuda, stream_p
 
 __all__ = [
     "SCALE_E8M0", "SCALE_F32", "scale_kind_of", "fp4_dequant_bf16", "fp8_dequant_bf16", "router_topk",
-    "moe_decode", "lm_head_accept", "expert_table", "shared_entry", "MAX_DECODE_TOKENS",
+    "moe_decode", "moe_layer_decode", "moe_layer_status", "lm_head_accept", "expert_table", "shared_entry",
+    "MAX_DECODE_TOKENS",
 ]
 
 MAX_DECODE_TOKENS = 8
@@ -184,6 +185,61 @@ def moe_decode_stage(stage: int, x: torch.Tensor, topk_idx: torch.Tensor, topk_w
                                   scale_kind, ptr(shared), ptr(out_f32), ptr(out_bf16), ptr(ws), ws.numel(),
                                   stream_ptr(dev))
     check(rc, f"moe_decode stage {stage}")
+
+
+def moe_layer_decode(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor | None, table: torch.Tensor,
+                     scale_kind: int, shared: torch.Tensor | None, i: int, top_k: int = 6, scaling: float = 1.5,
+                     swiglu_limit: float = 10.0, out_bf16: torch.Tensor | None = None,
+                     out_f32: torch.Tensor | None = None, idx_out: torch.Tensor | None = None,
+                     w_out: torch.Tensor | None = None, want_logits: bool = False):
+    """Router + routed experts + shared expert of one layer for M <= 8 tokens in
+    one launch; returns (out_bf16, out_f32, idx, w[, logits]).
+
+    Same results as router_topk followed by moe_decode.  Inputs must already be
+    contiguous device tensors of the right dtypes when called inside a graph
+    capture (no conversions are enqueued then)."""
+    dev = require_cuda(x, gate_w, gate_bias, table, shared)
+    if x.dtype != torch.bfloat16 or gate_w.dtype != torch.bfloat16:
+        raise TypeError("hidden states and gate weight must be bf16")
+    x = x.contiguous()
+    gate_w = gate_w.contiguous()
+    m, d = x.shape
+    n_exp = gate_w.shape[0]
+    if gate_w.shape[1] != d:
+        raise ValueError(f"gate weight {tuple(gate_w.shape)} does not match hidden size {d}")
+    if m > MAX_DECODE_TOKENS:
+        raise ValueError(f"moe_layer_decode handles at most {MAX_DECODE_TOKENS} tokens, got {m}")
+    if gate_bias is not None:
+        gate_bias = gate_bias.to(torch.float32).contiguous()
+    if idx_out is None:
+        idx_out = torch.empty(m, top_k, dtype=torch.int64, device=dev)
+    if w_out is None:
+        w_out = torch.empty(m, top_k, dtype=torch.float32, device=dev)
+    if tuple(idx_out.shape) != (m, top_k) or tuple(w_out.shape) != (m, top_k):
+        raise ValueError("idx_out / w_out must be [M, top_k]")
+    if out_bf16 is None and out_f32 is None:
+        out_bf16 = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
+    logits = torch.empty(m, n_exp, dtype=torch.bfloat16, device=dev) if want_logits else None
+    nbytes = lib().hsmoe_moe_layer_workspace_size(m, d, i, n_exp, top_k)
+    ws = _workspace(dev, "layer", nbytes)
+    rc = lib().hsmoe_moe_layer_decode(ptr(x), m, d, i, ptr(gate_w), ptr(gate_bias), n_exp, top_k, scaling,
+                                      ptr(table), scale_kind, ptr(shared), swiglu_limit, ptr(idx_out), ptr(w_out),
+                                      ptr(logits), ptr(out_f32), ptr(out_bf16), ptr(ws), ws.numel(),
+                                      stream_ptr(dev))
+    check(rc, "hsmoe_moe_layer_decode")
+    res = (out_bf16, out_f32, idx_out, w_out)
+    return res + (logits,) if want_logits else res
+
+
+def moe_layer_status(device: torch.device | None = None) -> int:
+    """The layer kernel's status word in this stream's workspace (0 = every
+    cross-workgroup wait completed).  Synchronises the device."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    ws = _workspaces.get((device.index, stream_ptr(device), "layer"))
+    if ws is None:
+        return 0
+    off = lib().hsmoe_moe_layer_status_offset()
+    return int(ws[off:off + 4].view(torch.int32).item())
 
 
 def lm_head_accept(h: torch.Tensor, lm_head: torch.Tensor, ids: torch.Tensor | None = None,

@@ -134,6 +134,36 @@ int hsmoe_moe_down(const void* x_dev, int64_t m, int64_t d, int64_t i, const int
                    void* workspace_dev, size_t workspace_bytes, hsmoe_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * One MoE layer at decode in a single persistent launch: the router of
+ * hsmoe_router_topk, then the routed experts and the shared expert of
+ * hsmoe_moe_decode, with no host round trip and no launch between them.
+ * Replaces HomeSeekInferenceEngine._forward_ffn for m <= 8 tokens (reference
+ * src/home_seek/inference_engine/engine.py:1410-1541): _compute_routing_experts
+ * (engine.py:1025-1031 -> src/home_seek/router.py:22-36), FusedMoEFFN.forward
+ * (src/home_seek/fused_moe.py:447-563) and the shared-expert add
+ * (engine.py:1530-1536).
+ * Inputs and results are those of the two calls it fuses, and bit-identical
+ * to them: x bf16 [m, d]; gate_w bf16 [n_experts, d]; gate_bias fp32
+ * [n_experts] or NULL; expert_table / scale_kind / shared as in
+ * hsmoe_moe_decode; topk_idx_out int64 [m, top_k] and topk_w_out fp32
+ * [m, top_k] receive the routing; logits_out bf16 [m, n_experts] or NULL;
+ * out_f32 / out_bf16 as in hsmoe_moe_decode.
+ * m in [1, 8], d % 512 == 0, d <= 8192, i % 512 == 0, n_experts <= 1024,
+ * top_k <= 16.  The workgroups hand work to each other through the workspace;
+ * the launch never has more workgroups than the device holds at once.  The
+ * uint32 at byte hsmoe_moe_layer_status_offset() of the workspace stays 0
+ * unless a cross-workgroup wait gave up (then the outputs are not valid).
+ */
+size_t hsmoe_moe_layer_workspace_size(int64_t m, int64_t d, int64_t i, int64_t n_experts, int top_k);
+int hsmoe_moe_layer_decode(const void* x_dev, int64_t m, int64_t d, int64_t i, const void* gate_w_dev,
+                           const float* gate_bias_dev, int64_t n_experts, int top_k, float routed_scaling,
+                           const uint64_t* expert_table_dev, int scale_kind, const uint64_t* shared_dev,
+                           float swiglu_limit, int64_t* topk_idx_out_dev, float* topk_w_out_dev,
+                           void* logits_out_dev, float* out_f32_dev, void* out_bf16_dev, void* workspace_dev,
+                           size_t workspace_bytes, hsmoe_stream_t stream);
+size_t hsmoe_moe_layer_status_offset(void);
+
+/* ---------------------------------------------------------------------------
  * lm_head logits + greedy argmax + longest-prefix draft acceptance.
  * Replaces the logits / acceptance loop of _mtp_verify_batched
  * (reference src/home_seek/inference_engine/engine.py:2480-2497) and the greedy

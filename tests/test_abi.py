@@ -36,3 +36,20 @@ def test_version_and_error_paths():
     assert rc == -4
     with pytest.raises(_lib.HsmoeError):
         _lib.check(rc, "lm_head")
+
+
+def test_layer_entry_point_rejects_bad_arguments():
+    """Argument and shape errors of the fused layer entry point are reported
+    before anything is launched (no GPU needed)."""
+    from home_seek_amd import _lib
+    L = _lib.lib()
+    rc = L.hsmoe_moe_layer_decode(4096, 1, 4096, 2048, None, None, 256, 6, 1.5, 4096, 0, None, 10.0, 4096, 4096,
+                                  None, 4096, None, 4096, 1 << 24, None)
+    assert rc == -1 and b"null" in L.hsmoe_last_error()
+    rc = L.hsmoe_moe_layer_decode(4096, 9, 4096, 2048, 4096, None, 256, 6, 1.5, 4096, 0, None, 10.0, 4096, 4096,
+                                  None, 4096, None, 4096, 1 << 24, None)
+    assert rc == -2 and b"m <= 8" in L.hsmoe_last_error()
+    rc = L.hsmoe_moe_layer_decode(4096, 1, 4096, 2048, 4096, None, 256, 6, 1.5, 4096, 0, None, 10.0, 4096, 4096,
+                                  None, 4096, None, 4096, 64, None)
+    assert rc == -4
+    assert L.hsmoe_moe_layer_workspace_size(1, 4096, 2048, 256, 6) > 0

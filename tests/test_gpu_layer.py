@@ -1,0 +1,143 @@
+"""GPU parity of the fused one-launch MoE layer (hsmoe_moe_layer_decode).
+
+The fused launch must reproduce router_topk followed by moe_decode bit for bit
+(same tiles, same accumulation order), and through them the fp32 oracle within
+the task's bar (rel-L2 <= 1e-3, max-abs <= 2e-2 on fp32 outputs).  Its
+cross-workgroup handoffs are exercised with calls of every m in [1, 8] sharing
+one workspace, absent experts, tables without a shared expert, and HIP graph
+replays checked replay by replay.
+"""
+import numpy as np
+import pytest
+import torch
+
+from home_seek_amd import expert_store, ops, synthetic
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+D, I, E, K, SEED = 4096, 2048, 256, 6, 31337
+
+
+@pytest.fixture(scope="module")
+def layer(dev):
+    store = expert_store.HbmExpertStore(1, E, D, I, dev, with_shared=True)
+    store.fill_synthetic(SEED)
+    gate, bias = synthetic.router_weights(SEED, 0, E, D, dev)
+    torch.cuda.synchronize()
+    return store, gate, bias
+
+
+def staged(x, gate, bias, table, shared):
+    idx, w = ops.router_topk(x, gate, bias, K, 1.5)
+    f32 = torch.empty(x.shape[0], D, dtype=torch.float32, device=x.device)
+    out, _ = ops.moe_decode(x, idx, w, table, ops.SCALE_E8M0, shared, 10.0, out_f32=f32, d=D, i=I)
+    return out, f32, idx, w
+
+
+def fused(x, gate, bias, table, shared, **kw):
+    """(out_bf16, out_f32, idx, w[, logits]) of the fused launch."""
+    f32 = torch.empty(x.shape[0], D, dtype=torch.float32, device=x.device)
+    res = ops.moe_layer_decode(x, gate, bias, table, ops.SCALE_E8M0, shared, I, K, 1.5, 10.0,
+                               out_bf16=torch.empty(x.shape[0], D, dtype=torch.bfloat16, device=x.device),
+                               out_f32=f32, **kw)
+    return (res[0], f32) + tuple(res[2:])
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_fused_layer_equals_staged_and_oracle(layer, dev, m):
+    store, gate, bias = layer
+    x = synthetic.hidden(SEED, 10 + m, m, D, dev)
+    a = fused(x, gate, bias, store.table(0), store.shared_entry(0))
+    b = staged(x, gate, bias, store.table(0), store.shared_entry(0))
+    torch.cuda.synchronize()
+    assert ops.moe_layer_status(dev) == 0
+    for got, ref, what in zip(a, b, ("bf16", "f32", "idx", "w")):
+        assert torch.equal(got, ref), what
+    xn = orc.to_np_bf16(x)
+    ridx, rw = orc.router(xn, orc.to_np_bf16(gate), bias.cpu().numpy(), K, 1.5)
+    assert np.array_equal(a[2].cpu().numpy(), ridx)
+    experts = {int(e): orc.gen_fp4_expert(SEED, 0, int(e), D, I) for e in np.unique(ridx)}
+    ref = orc.moe_layer_fp32(xn, ridx, a[3].cpu().numpy(), experts, orc.gen_shared_expert(SEED, 0, D, I), 10.0)
+    got = a[1].cpu().numpy().astype(np.float64)
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    mx = np.abs(got - ref).max()
+    print(f"[fused layer M={m}] rel-L2 {rel:.3e} max-abs {mx:.3e}")
+    assert rel <= 1e-3 and mx <= 2e-2
+
+
+def test_fused_layer_logits_and_every_m_sharing_a_workspace(layer, dev):
+    store, gate, bias = layer
+    for m in (8, 1, 5, 2, 7, 3, 6, 4, 1):
+        x = synthetic.hidden(SEED, 100 + m, m, D, dev)
+        a = fused(x, gate, bias, store.table(0), store.shared_entry(0), want_logits=True)
+        _, _, ref_logits = ops.router_topk(x, gate, bias, K, 1.5, want_logits=True)
+        b = staged(x, gate, bias, store.table(0), store.shared_entry(0))
+        torch.cuda.synchronize()
+        assert torch.equal(a[4], ref_logits), m
+        for got, ref, what in zip(a[:4], b, ("bf16", "f32", "idx", "w")):
+            assert torch.equal(got, ref), (m, what)
+    assert ops.moe_layer_status(dev) == 0
+
+
+def test_fused_layer_absent_experts_no_shared_no_bias(layer, dev):
+    """Absent table entries are skipped (a loader returning None), a layer
+    without a shared expert, and a router without bias."""
+    store, gate, bias = layer
+    x = synthetic.hidden(SEED, 200, 3, D, dev)
+    idx, _ = ops.router_topk(x, gate, None, K, 1.5)
+    table = store.table(0).clone()
+    drop = idx.reshape(-1)[::4]
+    table[drop] = 0
+    a = fused(x, gate, None, table, None)
+    b = staged(x, gate, None, table, None)
+    torch.cuda.synchronize()
+    assert ops.moe_layer_status(dev) == 0
+    for got, ref, what in zip(a, b, ("bf16", "f32", "idx", "w")):
+        assert torch.equal(got, ref), what
+    # every expert absent: the output is zero
+    z = fused(x, gate, None, torch.zeros_like(table), None)
+    zs = staged(x, gate, None, torch.zeros_like(table), None)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(z[1]) == 0 and torch.count_nonzero(z[0]) == 0
+    assert torch.count_nonzero(zs[1]) == 0 and torch.count_nonzero(zs[0]) == 0
+
+
+def test_fused_layer_graph_replays(layer, dev):
+    """Captured in a HIP graph and replayed, with eager work and host syncs
+    between replays; every replay must equal the eager result."""
+    store, gate, bias = layer
+    xs = [synthetic.hidden(SEED, 300 + j, 1, D, dev) for j in range(3)]
+    outs = [torch.empty(1, D, dtype=torch.float32, device=dev) for _ in range(3)]
+    idxs = [torch.empty(1, K, dtype=torch.int64, device=dev) for _ in range(3)]
+    ws = [torch.empty(1, K, dtype=torch.float32, device=dev) for _ in range(3)]
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for j in range(3):
+            ops.moe_layer_decode(xs[j], gate, bias, store.table(0), ops.SCALE_E8M0, store.shared_entry(0), I,
+                                 out_f32=outs[j], idx_out=idxs[j], w_out=ws[j])
+        torch.cuda.synchronize()
+        eager = [o.clone() for o in outs]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for j in range(3):
+                ops.moe_layer_decode(xs[j], gate, bias, store.table(0), ops.SCALE_E8M0, store.shared_entry(0), I,
+                                     out_f32=outs[j], idx_out=idxs[j], w_out=ws[j])
+    for rep in range(4):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for j in range(3):
+            assert torch.equal(outs[j], eager[j]), (rep, j)
+        staged(xs[rep % 3], gate, bias, store.table(0), store.shared_entry(0))  # eager work in between
+        torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        assert ops.moe_layer_status(dev) == 0
+
+
+def test_fused_layer_rejects_bad_shapes(layer, dev):
+    store, gate, bias = layer
+    x = synthetic.hidden(SEED, 400, 9, D, dev)
+    with pytest.raises(ValueError):
+        ops.moe_layer_decode(x, gate, bias, store.table(0), ops.SCALE_E8M0, None, I)
