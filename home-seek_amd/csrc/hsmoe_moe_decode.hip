@@ -218,10 +218,7 @@ __global__ void __launch_bounds__(64 * kP2Waves) moe_down_kernel(DecodeParams p)
   const int rows = 16 * kP2Waves;
   for (int q = threadIdx.x; q < rows * p.m; q += blockDim.x) {
     const int t = q / rows, d = blockIdx.x * rows + (q - t * rows);
-    float v = 0.0f;
-    for (int ss = 0; ss < n_slots; ++ss)
-      v = __fadd_rn(v, __hip_atomic_load(p.part + ((int64_t)ss * p.m + t) * p.d + d, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT));
+    const float v = sum_slots_agent(p.part + (int64_t)t * p.d + d, (int64_t)p.m * p.d, n_slots, nullptr);
     const int64_t o = (int64_t)t * p.d + d;
     if (p.out_f32) p.out_f32[o] = v;
     if (p.out_bf16) p.out_bf16[o] = (uint16_t)f32_to_bf16_bits(v);

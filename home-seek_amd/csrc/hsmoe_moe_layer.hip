@@ -10,13 +10,19 @@
 // accumulation order), so the results are bit-identical to those two calls.
 //
 // Work items, in dependency order (item q only ever waits on items < q):
-//   R    router rows: 4 expert rows per item (one per wave); the last R item
-//        to finish runs the top-k of every token and publishes the slot plan
-//        (distinct valid expert ids ascending, per-token slot weights)
+//   R    router rows: 4 expert rows per item (one per wave), published as
+//        fp32 scores; the last R item to finish also writes the routing
+//        outputs (top-k ids and weights)
 //   SGU  shared-expert gate/up, 16 rows of W1 and W3 per item
-//   GU   routed gate/up, (slot, 16 rows) per item; waits for the plan
-//   SD   shared-expert down, 64 rows of W2 per item
+//   SD   shared-expert down, 64 rows of W2 per item (ahead of the routed
+//        items: its weights stream while the routing is still being decided)
+//   GU   routed gate/up, (slot, 16 rows) per item; needs the slot plan
 //   D    routed down, (slot, 64 rows) per item
+// Every workgroup that runs a routed item (or the shared down) first builds the
+// slot plan itself, once per launch, in LDS: it waits for all R items, loads
+// the scores, runs the top-k of every token and lists the distinct valid
+// expert ids ascending with their per-token weights (the same deterministic
+// computation in every workgroup, so all plans agree).
 // A down item issues its first W2 loads, then waits until every gate/up item
 // of its slot has published the slot's activations, then stages them in LDS.
 // The last down item of a row group adds the slots' partials in slot order
@@ -40,6 +46,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxTok = 8;
 constexpr int kMaxSlots = 128;  // m * top_k routed slots; slot kMaxSlots is never used as routed
+constexpr int kMaxExperts = 256;
 constexpr int kGuRows = 16;
 constexpr int kDownRows = 16 * kWaves;
 constexpr unsigned kSpinLimit = 1u << 16;
@@ -48,23 +55,26 @@ constexpr unsigned kSpinLimit = 1u << 16;
 // that fix, cause not yet shown).  The entry point returns an error instead.
 constexpr bool kLayerKernelEnabled = true;
 
-// control words (unsigned) at the start of the workspace
+// Control words (unsigned) at the start of the workspace.  Counters take the
+// atomic increments; waiters never poll a counter.  The producer that
+// completes a counter instead sets a flag, written in kFlagCopies copies 4 KiB
+// apart (workgroup b polls copy b % kFlagCopies), so that polling spreads over
+// several memory channels and never contends with the increments.
 constexpr int kCtlRouter = 0;    // router items finished
-constexpr int kCtlPlan = 64;     // 1 once the slot plan is published
 constexpr int kCtlDone = 128;    // workgroups finished
 constexpr int kCtlErr = 192;     // sticky: 1 + index of a control word whose wait gave up
 constexpr int kCtlSlot = 256;    // + 16*s: gate/up items of slot s finished
 constexpr int kCtlRowGroup = kCtlSlot + 16 * (kMaxSlots + 1);  // + g: down items of row group g finished
 constexpr int kMaxRowGroups = 2048;
-constexpr size_t kCtlBytes = 32768;
-static_assert((kCtlRowGroup + kMaxRowGroups) * 4 <= (int)kCtlBytes, "control block overflow");
-
-struct PlanG {
-  int n_routed;
-  int pad[63];
-  int eid[kMaxSlots];
-  float wt[kMaxSlots][kMaxTok];
-};
+constexpr int kFlagCopies = 8;
+constexpr int kFlagBase = 8192;      // word index of flag copy 0 (32 KiB)
+constexpr int kFlagStride = 1024;    // words between copies (4 KiB)
+constexpr int kFlagRouter = 0;       // + copy: every router item finished
+constexpr int kFlagSlot = 16;        // + 4*s: every gate/up item of slot s finished
+constexpr size_t kCtlBytes = 65536;
+static_assert(kCtlRowGroup + kMaxRowGroups <= kFlagBase, "control block overflow");
+static_assert(kFlagSlot + 4 * (kMaxSlots + 1) <= kFlagStride, "flag block overflow");
+static_assert((kFlagBase + kFlagCopies * kFlagStride) * 4 <= (int)kCtlBytes, "flag copies overflow");
 
 struct LayerParams {
   const uint16_t* x;       // bf16 [m, d]
@@ -82,99 +92,122 @@ struct LayerParams {
   uint16_t* out_bf16;  // [m, d] or null
   unsigned* ctl;
   float* scores;  // [m][n_exp]
-  PlanG* plan;
   float* act;   // fp32 [S + 1][m][i] weighted activations (slot S = shared)
   float* part;  // fp32 [S + 1][m][d] per-slot down partials
-  int n_router, q_sgu, q_gu, q_sd, q_down, n_items;
+  int n_router, q_sgu, q_sd, q_gu, q_down, n_items;  // item ranges: R, SGU, SD, GU, D
 };
 
-__device__ bool wait_at_least(unsigned* ctl, int word, unsigned target) {
+// Waits (one thread) until this workgroup's copy of flag `flag` is set;
+// polls with backoff.  Gives up after kSpinLimit polls, recording the flag.
+__device__ bool wait_flag(unsigned* ctl, int flag) {
+  const unsigned* f = ctl + kFlagBase + (int)(blockIdx.x % kFlagCopies) * kFlagStride + flag;
+  int nap = 1;
   for (unsigned it = 0; it < kSpinLimit; ++it) {
-    if (load_agent(ctl + word) >= target) return true;
-    __builtin_amdgcn_s_sleep(2);
+    if (load_agent(f) != 0u) return true;
+    if (nap == 1) __builtin_amdgcn_s_sleep(1);
+    else if (nap == 2) __builtin_amdgcn_s_sleep(2);
+    else if (nap == 4) __builtin_amdgcn_s_sleep(4);
+    else if (nap == 8) __builtin_amdgcn_s_sleep(8);
+    else __builtin_amdgcn_s_sleep(16);
+    nap = nap < 16 ? 2 * nap : 16;
   }
-  store_agent(ctl + kCtlErr, 1u + (unsigned)word);
+  store_agent(ctl + kCtlErr, 1u + (unsigned)(kFlagBase + flag));
   return false;
+}
+
+// Sets every copy of flag `flag` (after the data it announces is complete).
+__device__ __forceinline__ void set_flag(unsigned* ctl, int flag) {
+  for (int c = 0; c < kFlagCopies; ++c) store_agent(ctl + kFlagBase + c * kFlagStride + flag, 1u);
 }
 
 struct Shared {
   float red[kWaves][2][256];
-  int64_t idx[kMaxSlots];
-  float w[kMaxSlots];
-  int cand[kMaxSlots];
-  int first[kMaxSlots];
-  float wt[kMaxTok];
+  int64_t idx[kMaxSlots];  // top-k ids of every token
+  float w[kMaxSlots];      // top-k weights of every token
+  int eid[kMaxSlots];            // slot plan: expert id of routed slot s
+  float wt[kMaxSlots][kMaxTok];  // slot plan: weight of routed slot s for token t
+  float wt_item[kMaxTok];
   int flag;
   int n_routed;
-  int eid;
-  int count;
+  int have_plan;
+  int wave_count[kWaves];
+  unsigned char valid[kMaxExperts];  // expert e has a table entry (filled at kernel start)
+  unsigned char used[kMaxExperts];   // expert e is selected by some token (plan build)
+  short rank[kMaxExperts];           // slot of a selected expert (plan build)
 };
 
-// Top-k of every token, then the slot plan; run by the last router item.
-__device__ __forceinline__ void publish_plan(const LayerParams& p, Shared& sh) {
-  const int wave = threadIdx.x >> 6;
+// The slot plan of this launch in LDS, built once per workgroup: waits for
+// every router item, then top-k of every token (one token per wave, ties to
+// the lower index) and the distinct valid expert ids in ascending order with
+// each token's weight for them (its top-k weights for that id, summed in k
+// order; the union of _forward_legacy, fused_moe.py:466-476).
+__device__ __forceinline__ void build_plan(const LayerParams& p, Shared& sh) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = p.m * p.top_k;
-  for (int t = wave; t < p.m; t += kWaves)
-    wave_topk(p.scores + (int64_t)t * p.n_exp, p.n_exp, p.top_k, p.scaling, sh.idx + t * p.top_k,
-              sh.w + t * p.top_k);
-  if (threadIdx.x == 0) sh.count = 0;
+  for (int e = threadIdx.x; e < p.n_exp; e += kThreads) sh.used[e] = 0;
+  if (threadIdx.x == 0) wait_flag(p.ctl, kFlagRouter);
+  __syncthreads();
+  // (n_exp <= kMaxExperts: at most 4 keys per lane)
+  for (int t = wave; t < p.m; t += kWaves) {
+    const float* sc = p.scores + (int64_t)t * p.n_exp;
+    if (p.n_exp <= 64) wave_topk_n<1>(sc, p.n_exp, p.top_k, p.scaling, sh.idx + t * p.top_k, sh.w + t * p.top_k);
+    else if (p.n_exp <= 128) wave_topk_n<2>(sc, p.n_exp, p.top_k, p.scaling, sh.idx + t * p.top_k, sh.w + t * p.top_k);
+    else wave_topk_n<4>(sc, p.n_exp, p.top_k, p.scaling, sh.idx + t * p.top_k, sh.w + t * p.top_k);
+  }
   __syncthreads();
   for (int j = threadIdx.x; j < n; j += kThreads) {
+    const int64_t e = sh.idx[j];
+    if (e >= 0 && e < p.n_exp && sh.valid[e]) sh.used[e] = 1;
+  }
+  __syncthreads();
+  // slots = selected experts in ascending id order: ballot prefix ranks
+  int base = 0;
+  for (int e0 = 0; e0 < p.n_exp; e0 += kThreads) {
+    const int e = e0 + threadIdx.x;
+    const bool u = e < p.n_exp && sh.used[e];
+    const uint64_t mask = __ballot(u);
+    const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+    if (lane == 0) sh.wave_count[wave] = __popcll(mask);
+    __syncthreads();
+    int off = base;
+    for (int w = 0; w < wave; ++w) off += sh.wave_count[w];
+    if (u) {
+      sh.rank[e] = (short)(off + below);
+      sh.eid[off + below] = e;
+    }
+    for (int w = 0; w < kWaves; ++w) base += sh.wave_count[w];
+    __syncthreads();
+  }
+  // each token's weight of each slot: its top-k weight for that expert (a
+  // token's top-k ids are distinct, so at most one), else 0
+  for (int c = threadIdx.x; c < base * p.m; c += kThreads) sh.wt[c / p.m][c % p.m] = 0.0f;
+  __syncthreads();
+  for (int j = threadIdx.x; j < n; j += kThreads) {
+    const int64_t e = sh.idx[j];
+    if (e >= 0 && e < p.n_exp && sh.valid[e]) sh.wt[sh.rank[e]][j / p.top_k] = __fadd_rn(0.0f, sh.w[j]);
+  }
+  if (threadIdx.x == 0) {
+    sh.n_routed = base;
+    sh.have_plan = 1;
+  }
+  __syncthreads();
+}
+
+// The routing outputs (and the zero output of a layer with no valid expert
+// and no shared expert), written once by the last router item.
+__device__ __forceinline__ void write_routing(const LayerParams& p, Shared& sh) {
+  for (int j = threadIdx.x; j < p.m * p.top_k; j += kThreads) {
     p.idx_out[j] = sh.idx[j];
     p.w_out[j] = sh.w[j];
-    const int64_t e = sh.idx[j];
-    const bool ok = e >= 0 && e < p.n_exp && p.table[e * 6] != 0;
-    sh.cand[j] = ok ? (int)e : -1;
   }
-  __syncthreads();
-  for (int j = threadIdx.x; j < n; j += kThreads) {
-    const int e = sh.cand[j];
-    bool first = e >= 0;
-    for (int q = 0; q < j && first; ++q) first = sh.cand[q] != e;
-    sh.first[j] = first;
-  }
-  __syncthreads();
-  for (int j = threadIdx.x; j < n; j += kThreads) {
-    if (sh.first[j]) {
-      const int e = sh.cand[j];
-      int rank = 0;
-      for (int q = 0; q < n; ++q) rank += (sh.first[q] && sh.cand[q] < e);
-      store_agent(&p.plan->eid[rank], e);
-      // the slot's weight for each token: its top-k weights for e, summed in k order
-      for (int t = 0; t < p.m; ++t) {
-        float w = 0.0f;
-        for (int k = 0; k < p.top_k; ++k)
-          if (sh.idx[t * p.top_k + k] == e) w = __fadd_rn(w, sh.w[t * p.top_k + k]);
-        store_agent(&p.plan->wt[rank][t], w);
-      }
-      atomicAdd(&sh.count, 1);
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) store_agent(&p.plan->n_routed, sh.count);
-  if (sh.count == 0 && !p.shared) {
-    // no valid expert and no shared expert: no down item will run, and the
-    // layer's output is zero (_forward_legacy returns zeros_like, fused_moe.py:473-474, 512-513)
+  if (sh.n_routed == 0 && !p.shared) {
+    // no down item will run, and the output is zero (_forward_legacy returns
+    // zeros_like, fused_moe.py:473-474, 512-513)
     for (int c = threadIdx.x; c < p.m * p.d; c += kThreads) {
       if (p.out_f32) p.out_f32[c] = 0.0f;
       if (p.out_bf16) p.out_bf16[c] = 0;
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) store_agent(p.ctl + kCtlPlan, 1u);
-}
-
-// Thread 0 waits for the plan and reads the slot count (and the expert id of
-// routed slot s, or -1); every thread returns with sh.n_routed / sh.eid set.
-__device__ __forceinline__ void read_plan(const LayerParams& p, Shared& sh, int s) {
-  if (threadIdx.x == 0) {
-    wait_at_least(p.ctl, kCtlPlan, 1u);
-    const int nr = load_agent(&p.plan->n_routed);
-    sh.n_routed = nr;
-    sh.eid = (s >= 0 && s < nr) ? load_agent(&p.plan->eid[s]) : -1;
-  }
-  __syncthreads();
 }
 
 
@@ -199,12 +232,29 @@ __device__ __forceinline__ LayerParams params(uint64_t kernarg) {
 #endif
 }
 
+// Builds the slot plan into g_sh (a function of its own, called from the
+// kernel's item loop, so the top-k state adds to no streaming item's
+// registers); the last router item also writes the routing outputs.
+__device__ __noinline__ void plan_item(uint64_t kernarg, int write_outputs) {
+  const LayerParams p = params(kernarg);
+  build_plan(p, g_sh);
+  if (__builtin_amdgcn_readfirstlane(write_outputs)) write_routing(p, g_sh);
+}
+
 // Copies x into the LDS tile unless it is already there (state: 1 = x in LDS).
 __device__ __forceinline__ void ensure_x(const LayerParams& p, int& state) {
   if (state == 1) return;
   const int n16 = p.m * p.d / 8;
-  for (int q = threadIdx.x; q < n16; q += kThreads)
-    reinterpret_cast<uint4*>(g_tile)[q] = reinterpret_cast<const uint4*>(p.x)[q];
+  const uint4* src = reinterpret_cast<const uint4*>(p.x);
+  for (int q0 = threadIdx.x; q0 < n16; q0 += 8 * kThreads) {
+    uint4 v[8];  // every load of the pass in flight before the first LDS store
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (q0 + j * kThreads < n16) v[j] = src[q0 + j * kThreads];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (q0 + j * kThreads < n16) reinterpret_cast<uint4*>(g_tile)[q0 + j * kThreads] = v[j];
+  }
   __syncthreads();
   state = 1;
 }
@@ -223,9 +273,11 @@ __device__ __noinline__ int router_item(uint64_t kernarg, int q_arg, int state_a
     router_row(wv, g_tile, p.m, p.d, e, p.n_exp, p.bias, p.logits ? p.logits + e : nullptr, p.scores + e);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) sh.flag = add_agent(p.ctl + kCtlRouter, 1u) == (unsigned)(p.n_router - 1);
+  if (threadIdx.x == 0) {
+    sh.flag = add_agent(p.ctl + kCtlRouter, 1u) == (unsigned)(p.n_router - 1);
+    if (sh.flag) set_flag(p.ctl, kFlagRouter);
+  }
   __syncthreads();
-  if (sh.flag) publish_plan(p, sh);
   return state;
 }
 
@@ -236,18 +288,13 @@ __device__ __noinline__ int gate_up_item(uint64_t kernarg, int q_arg, int state_
   Shared& sh = g_sh;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int gu_per_slot = p.i / kGuRows;
-  const bool is_shared = q < p.q_gu;
+  const bool is_shared = q < p.q_sd;
   const int qq = is_shared ? q - p.q_sgu : q - p.q_gu;
   const int s = is_shared ? p.S : qq / gu_per_slot;
   const int r0 = (qq % gu_per_slot) * kGuRows;
-  if (!is_shared) {
-    read_plan(p, sh, s);
-    if (s >= sh.n_routed) return state;
-    if (threadIdx.x < p.m) sh.wt[threadIdx.x] = load_agent(&p.plan->wt[s][threadIdx.x]);
-  } else if (threadIdx.x < p.m) {
-    sh.wt[threadIdx.x] = 1.0f;
-  }
-  const uint64_t* ent = is_shared ? p.shared : p.table + (int64_t)sh.eid * 6;
+  if (!is_shared && s >= sh.n_routed) return state;
+  if (threadIdx.x < p.m) sh.wt_item[threadIdx.x] = is_shared ? 1.0f : sh.wt[s][threadIdx.x];
+  const uint64_t* ent = is_shared ? p.shared : p.table + (int64_t)sh.eid[s] * 6;
   ensure_x(p, state);
   const int per = (p.d / 128) / kWaves;
   const int st0 = wave * per;
@@ -268,46 +315,64 @@ __device__ __noinline__ int gate_up_item(uint64_t kernarg, int q_arg, int state_
       gsum = __fadd_rn(gsum, sh.red[w][0][threadIdx.x]);
       usum = __fadd_rn(usum, sh.red[w][1][threadIdx.x]);
     }
-    const float a = __fmul_rn(sh.wt[col], swiglu(gsum, usum, p.limit));
+    const float a = __fmul_rn(sh.wt_item[col], swiglu(gsum, usum, p.limit));
     store_agent(p.act + ((int64_t)s * p.m + col) * p.i + r0 + row, a);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) add_agent(p.ctl + kCtlSlot + 16 * s, 1u);
+  if (threadIdx.x == 0 && add_agent(p.ctl + kCtlSlot + 16 * s, 1u) == (unsigned)(gu_per_slot - 1))
+    set_flag(p.ctl, kFlagSlot + 4 * s);
   return state;
 }
 
+// Slot and row group of down item q (shared down items first).
+__device__ __forceinline__ void down_slot_of(const LayerParams& p, int q, bool& is_shared, int& s, int& g) {
+  const int down_per_slot = p.d / kDownRows;
+  is_shared = q < p.q_gu;
+  const int qq = is_shared ? q - p.q_sd : q - p.q_down;
+  s = is_shared ? p.S : qq / down_per_slot;
+  g = qq % down_per_slot;
+}
+
+// Down item q, first part: W2 rows of the slot against its activations, the
+// slot's fp32 partial sums written for the row group.  Needs the slot plan
+// for a routed slot only (the shared slot runs before the plan exists).
 __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg) {
   const int q = __builtin_amdgcn_readfirstlane(q_arg);
   int state = __builtin_amdgcn_readfirstlane(state_arg);
   const LayerParams p = params(kernarg);
   Shared& sh = g_sh;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int gu_per_slot = p.i / kGuRows, down_per_slot = p.d / kDownRows;
-  const bool is_shared = q < p.q_down;
-  const int qq = is_shared ? q - p.q_sd : q - p.q_down;
-  const int s = is_shared ? p.S : qq / down_per_slot;
-  const int g = qq % down_per_slot;
-  read_plan(p, sh, is_shared ? -1 : s);
+  bool is_shared;
+  int s, g;
+  down_slot_of(p, q, is_shared, s, g);
   if (!is_shared && s >= sh.n_routed) return state;
-  const int n_routed = sh.n_routed;
-  const uint64_t* ent = is_shared ? p.shared : p.table + (int64_t)sh.eid * 6;
+  const uint64_t* ent = is_shared ? p.shared : p.table + (int64_t)sh.eid[s] * 6;
   const int r0 = g * kDownRows + 16 * wave;
   const int m = p.m, i = p.i;
   unsigned* const ctl = p.ctl;
   const float* const src = p.act + (int64_t)s * m * i;
   f32x4 acc = {0, 0, 0, 0};
   down_slot(slot_format(p.scale_fmt, ent, is_shared), ent, g_tile, m, i, r0, acc, [&]() __attribute__((always_inline)) {
-    if (threadIdx.x == 0) wait_at_least(ctl, kCtlSlot + 16 * s, (unsigned)gu_per_slot);
+    if (threadIdx.x == 0) wait_flag(ctl, kFlagSlot + 4 * s);
     __syncthreads();
     // fp32 activations -> bf16 hi rows [t][k] and lo rows [m + t][k]
+    // (8 loads in flight per thread before any is used)
     const int n = m * i;
-    for (int c = threadIdx.x; c < n; c += kThreads) {
-      const float a = load_agent(src + c);
-      const uint32_t hi = f32_to_bf16_bits(a);
-      const uint32_t lo = f32_to_bf16_bits(__fadd_rn(a, -bf16_bits_to_f32(hi)));
-      g_tile[c] = (uint16_t)hi;
-      g_tile[n + c] = (uint16_t)lo;
+    for (int c0 = threadIdx.x; c0 < n; c0 += 8 * kThreads) {
+      float a[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a[j] = (c0 + j * kThreads < n) ? load_agent(src + c0 + j * kThreads) : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int c = c0 + j * kThreads;
+        if (c < n) {
+          const uint32_t hi = f32_to_bf16_bits(a[j]);
+          const uint32_t lo = f32_to_bf16_bits(__fadd_rn(a[j], -bf16_bits_to_f32(hi)));
+          g_tile[c] = (uint16_t)hi;
+          g_tile[n + c] = (uint16_t)lo;
+        }
+      }
     }
     __syncthreads();
   });
@@ -323,32 +388,68 @@ __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  return state;
+}
+
+// Down item q, second part (the slot plan exists): arrival on the row group;
+// the last slot to arrive adds the slots' partials in slot order (routed
+// ascending, shared last) and writes the output rows.
+__device__ __noinline__ void down_finish(uint64_t kernarg, int q_arg) {
+  const int q = __builtin_amdgcn_readfirstlane(q_arg);
+  const LayerParams p = params(kernarg);
+  Shared& sh = g_sh;
+  bool is_shared;
+  int s, g;
+  down_slot_of(p, q, is_shared, s, g);
+  const int n_routed = sh.n_routed;
+  if (!is_shared && s >= n_routed) return;
+  const int m = p.m;
   const int n_slots = n_routed + (p.shared ? 1 : 0);
   if (threadIdx.x == 0) sh.flag = add_agent(p.ctl + kCtlRowGroup + g, 1u) == (unsigned)(n_slots - 1);
   __syncthreads();
   if (sh.flag) {
     for (int c = threadIdx.x; c < kDownRows * m; c += kThreads) {
       const int t = c / kDownRows, dd = g * kDownRows + (c - t * kDownRows);
-      float v = 0.0f;
-      for (int ss = 0; ss < n_routed; ++ss) v = __fadd_rn(v, load_agent(p.part + ((int64_t)ss * m + t) * p.d + dd));
-      if (p.shared) v = __fadd_rn(v, load_agent(p.part + ((int64_t)p.S * m + t) * p.d + dd));
+      const float v = sum_slots_agent(p.part + (int64_t)t * p.d + dd, (int64_t)m * p.d, n_routed,
+                                      p.shared ? p.part + ((int64_t)p.S * m + t) * p.d + dd : nullptr);
       const int64_t o = (int64_t)t * p.d + dd;
       if (p.out_f32) p.out_f32[o] = v;
       if (p.out_bf16) p.out_bf16[o] = (uint16_t)f32_to_bf16_bits(v);
     }
   }
-  return state;
 }
 
 __global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
   int state = 0;  // 1 while the LDS tile holds x
+  if (threadIdx.x == 0) g_sh.have_plan = 0;
+  // which experts the table holds (for the slot plan), read once up front
+  for (int e = threadIdx.x; e < p.n_exp; e += kThreads) g_sh.valid[e] = p.table[(int64_t)e * 6] != 0;
   const uint64_t kernarg = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();  // &p
-  const int n_items = p.n_items, q_sgu = p.q_sgu, q_sd = p.q_sd;
+  const int n_items = p.n_items, q_sgu = p.q_sgu, q_sd = p.q_sd, q_gu = p.q_gu, q_down = p.q_down;
   for (int q = blockIdx.x; q < n_items; q += gridDim.x) {
     __syncthreads();  // the previous item's readers of the LDS scratch are done
-    if (q < q_sgu) state = router_item(kernarg, q, state);
-    else if (q < q_sd) state = gate_up_item(kernarg, q, state);
-    else state = down_item(kernarg, q, state);
+    if (q < q_sgu) {
+      state = router_item(kernarg, q, state);
+      if (g_sh.flag) plan_item(kernarg, 1);  // the last router item
+      continue;
+    }
+    if (q < q_sd) {  // shared gate/up
+      state = gate_up_item(kernarg, q, state);
+      continue;
+    }
+    if (q < q_gu) {  // shared down: the plan is needed only for its arrival
+      state = down_item(kernarg, q, state);
+      if (!g_sh.have_plan) plan_item(kernarg, 0);
+      down_finish(kernarg, q);
+      continue;
+    }
+    if (!g_sh.have_plan) plan_item(kernarg, 0);  // routed items need the slot plan
+    if (q < q_down) {
+      state = gate_up_item(kernarg, q, state);
+    } else {
+      state = down_item(kernarg, q, state);
+      down_finish(kernarg, q);
+    }
   }
   // the last workgroup to finish re-arms every control word for the next call
   __builtin_amdgcn_s_waitcnt(0);
@@ -358,16 +459,18 @@ __global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
   if (!g_sh.flag) return;
   if (threadIdx.x == 0) {
     store_agent(p.ctl + kCtlRouter, 0u);
-    store_agent(p.ctl + kCtlPlan, 0u);
     store_agent(p.ctl + kCtlDone, 0u);
   }
   for (int s = threadIdx.x; s <= p.S; s += kThreads) store_agent(p.ctl + kCtlSlot + 16 * s, 0u);
   for (int g = threadIdx.x; g < p.d / kDownRows; g += kThreads) store_agent(p.ctl + kCtlRowGroup + g, 0u);
+  for (int c = threadIdx.x; c < kFlagCopies * (p.S + 2); c += kThreads) {
+    const int copy = c % kFlagCopies, f = c / kFlagCopies;  // f = 0: router, f = 1 + s: slot s
+    store_agent(p.ctl + kFlagBase + copy * kFlagStride + (f == 0 ? kFlagRouter : kFlagSlot + 4 * (f - 1)), 0u);
+  }
 }
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 size_t scores_bytes(int64_t m, int64_t n_exp) { return align256((size_t)(m * n_exp * 4)); }
-size_t plan_bytes() { return align256(sizeof(PlanG)); }
 size_t act_bytes(int64_t m, int64_t i, int top_k) { return align256((size_t)(m * top_k + 1) * m * i * 4); }
 size_t part_bytes(int64_t m, int64_t d, int top_k) { return align256((size_t)(m * top_k + 1) * m * d * 4); }
 
@@ -411,7 +514,7 @@ using namespace hsmoe;
 
 extern "C" size_t hsmoe_moe_layer_workspace_size(int64_t m, int64_t d, int64_t i, int64_t n_experts, int top_k) {
   if (m < 1 || d < 1 || i < 1 || n_experts < 1 || top_k < 1) return 0;
-  return kCtlBytes + scores_bytes(m, n_experts) + plan_bytes() + act_bytes(m, i, top_k) + part_bytes(m, d, top_k);
+  return kCtlBytes + scores_bytes(m, n_experts) + act_bytes(m, i, top_k) + part_bytes(m, d, top_k);
 }
 
 extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
@@ -429,9 +532,9 @@ extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64
     return fail(HSMOE_ERR_ARG, "%s: null pointer or no output", name);
   if (scale_kind != HSMOE_SCALE_E8M0 && scale_kind != HSMOE_SCALE_F32)
     return fail(HSMOE_ERR_ARG, "%s: unknown scale_kind %d", name, scale_kind);
-  if (m < 1 || m > kMaxTok || n_experts < 1 || n_experts > 1024 || top_k < 1 || top_k > 16 || top_k > n_experts ||
-      m * top_k > kMaxSlots)
-    return fail(HSMOE_ERR_SHAPE, "%s: need 1 <= m <= 8, n_experts <= 1024, 1 <= top_k <= min(16, n_experts)", name);
+  if (m < 1 || m > kMaxTok || n_experts < 1 || n_experts > kMaxExperts || top_k < 1 || top_k > 16 ||
+      top_k > n_experts || m * top_k > kMaxSlots)
+    return fail(HSMOE_ERR_SHAPE, "%s: need 1 <= m <= 8, n_experts <= 256, 1 <= top_k <= min(16, n_experts)", name);
   if (d % 512 != 0 || i % 512 != 0 || d <= 0 || i <= 0 || d > 8192 || d / kDownRows > kMaxRowGroups)
     return fail(HSMOE_ERR_SHAPE, "%s: d and i must be positive multiples of 512, d <= 8192 (d=%lld i=%lld)", name,
                 (long long)d, (long long)i);
@@ -467,17 +570,15 @@ extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64
   ws += kCtlBytes;
   p.scores = (float*)ws;
   ws += scores_bytes(m, n_experts);
-  p.plan = (PlanG*)ws;
-  ws += plan_bytes();
   p.act = (float*)ws;
   ws += act_bytes(m, i, top_k);
   p.part = (float*)ws;
   const int has_shared = shared ? 1 : 0;
   p.n_router = (int)((n_experts + kWaves - 1) / kWaves);
   p.q_sgu = p.n_router;
-  p.q_gu = p.q_sgu + has_shared * (int)(i / kGuRows);
-  p.q_sd = p.q_gu + p.S * (int)(i / kGuRows);
-  p.q_down = p.q_sd + has_shared * (int)(d / kDownRows);
+  p.q_sd = p.q_sgu + has_shared * (int)(i / kGuRows);
+  p.q_gu = p.q_sd + has_shared * (int)(d / kDownRows);
+  p.q_down = p.q_gu + p.S * (int)(i / kGuRows);
   p.n_items = p.q_down + p.S * (int)(d / kDownRows);
   int resident = 0;
   int rc = resident_workgroups(lds, &resident);

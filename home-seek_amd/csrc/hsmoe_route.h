@@ -31,50 +31,78 @@ __device__ __forceinline__ uint64_t score_key(float v, int e) {
   return ((uint64_t)b << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint64_t o = __shfl_xor(k, off, 64);
-    k = o > k ? o : k;
-  }
-  return k;
+// One DPP step of a wave-wide 64-bit max: every lane enabled by kRowMask
+// takes the larger of its key and the key of the lane kCtrl names.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint64_t dpp_max_step(uint64_t k) {
+  const int lo = (int)(uint32_t)k, hi = (int)(uint32_t)(k >> 32);
+  const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, kCtrl, kRowMask, 0xf, false);
+  const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, kCtrl, kRowMask, 0xf, false);
+  const uint64_t o = ((uint64_t)ohi << 32) | olo;
+  return o > k ? o : k;
 }
 
-// Top-k of one token by one wave: lane l keys experts l, l+64, ...; each round
-// retires the wave-wide maximum key.  `sc` holds the token's fp32 scores,
-// written by other blocks and read with agent-scope loads.
-__device__ __forceinline__ void wave_topk(const float* sc, int64_t n_exp, int top_k, float scaling, int64_t* idx_out,
-                          float* w_out) {
+// Wave-wide maximum of a 64-bit key, returned to every lane: quad swaps,
+// half-row and row mirrors, then the row broadcasts of lane 15 and lane 31
+// leave the maximum in lane 63 (six dependent DPP steps instead of six
+// LDS-crossbar shuffles).
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+  k = dpp_max_step<0xb1, 0xf>(k);   // quad_perm [1,0,3,2]
+  k = dpp_max_step<0x4e, 0xf>(k);   // quad_perm [2,3,0,1]
+  k = dpp_max_step<0x141, 0xf>(k);  // row_half_mirror
+  k = dpp_max_step<0x140, 0xf>(k);  // row_mirror
+  k = dpp_max_step<0x142, 0xa>(k);  // row_bcast:15 into rows 1, 3
+  k = dpp_max_step<0x143, 0xc>(k);  // row_bcast:31 into rows 2, 3
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Top-k of one token by one wave: lane l keys experts l, l+64, ... (kPer of
+// them, sorted descending once), and each round retires the wave-wide maximum
+// key, popping it from the head of its lane's list.  `sc` holds the token's
+// fp32 scores, written by other workgroups and read with agent-scope loads.
+template <int kPer>
+__device__ __forceinline__ void wave_topk_n(const float* sc, int64_t n_exp, int top_k, float scaling,
+                                            int64_t* idx_out, float* w_out) {
   const int lane = threadIdx.x & 63;
-  const int per = (int)((n_exp + 63) / 64);
-  uint64_t key[kMaxPerLane];
+  float v[kPer];  // every load is issued before any is used (one memory round trip)
 #pragma unroll
-  for (int q = 0; q < kMaxPerLane; ++q) {
+  for (int q = 0; q < kPer; ++q) {
     const int e = lane + 64 * q;
-    key[q] = (q < per && e < n_exp)
-                 ? score_key(__hip_atomic_load(sc + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), e)
-                 : 0ull;
+    v[q] = __hip_atomic_load(sc + (e < n_exp ? e : n_exp - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  uint64_t key[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int e = lane + 64 * q;
+    key[q] = e < n_exp ? score_key(v[q], e) : 0ull;
+  }
+#pragma unroll
+  for (int i = 1; i < kPer; ++i)  // insertion network, descending
+#pragma unroll
+    for (int j = i; j > 0; --j) {
+      const uint64_t a = key[j - 1], b = key[j];
+      key[j - 1] = a > b ? a : b;
+      key[j] = a > b ? b : a;
+    }
   float my_v = 0.0f, sum = 0.0f;
   int my_e = 0;
   for (int r = 0; r < top_k; ++r) {
-    uint64_t best = 0;
+    const uint64_t best = wave_max_u64(key[0]);
+    const bool mine = key[0] == best;  // keys are unique: one lane
 #pragma unroll
-    for (int q = 0; q < kMaxPerLane; ++q)
-      if (q < per) best = key[q] > best ? key[q] : best;
-    best = wave_max_u64(best);
+    for (int q = 0; q + 1 < kPer; ++q) key[q] = mine ? key[q + 1] : key[q];
+    key[kPer - 1] = mine ? 0ull : key[kPer - 1];
     const int e = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
-#pragma unroll
-    for (int q = 0; q < kMaxPerLane; ++q)
-      if (q < per && lane + 64 * q == e) key[q] = 0ull;
     uint32_t b = (uint32_t)(best >> 32);
     b = (b & 0x80000000u) ? (b & 0x7fffffffu) : ~b;  // undo score_key's float map
-    const float v = __uint_as_float(b);
+    const float val = __uint_as_float(b);
     if (lane == r) {
-      my_v = v;
+      my_v = val;
       my_e = e;
     }
-    sum = __fadd_rn(sum, v);
+    sum = __fadd_rn(sum, val);
   }
   sum = fmaxf(sum, 1e-20f);
   if (lane < top_k) {
@@ -83,6 +111,15 @@ __device__ __forceinline__ void wave_topk(const float* sc, int64_t n_exp, int to
   }
 }
 
+__device__ __forceinline__ void wave_topk(const float* sc, int64_t n_exp, int top_k, float scaling, int64_t* idx_out,
+                                          float* w_out) {
+  const int per = (int)((n_exp + 63) / 64);
+  if (per <= 1) wave_topk_n<1>(sc, n_exp, top_k, scaling, idx_out, w_out);
+  else if (per <= 2) wave_topk_n<2>(sc, n_exp, top_k, scaling, idx_out, w_out);
+  else if (per <= 4) wave_topk_n<4>(sc, n_exp, top_k, scaling, idx_out, w_out);
+  else if (per <= 8) wave_topk_n<8>(sc, n_exp, top_k, scaling, idx_out, w_out);
+  else wave_topk_n<16>(sc, n_exp, top_k, scaling, idx_out, w_out);
+}
 
 // One wave computes the router logit and score of expert row `e` for the nt
 // (<= 8) token rows of xs ([nt][d] bf16 in LDS); `wv` holds the row's lane

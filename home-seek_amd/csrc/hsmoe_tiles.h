@@ -271,4 +271,22 @@ __device__ __forceinline__ unsigned add_agent(unsigned* p, unsigned v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Fixed-order sum over n slots of agent-scope values base[s * stride]
+// (s = 0 .. n-1, then `extra` when non-null): the loads go out 8 at a time so
+// a chain of them costs one memory round trip per 8 slots, and the additions
+// keep slot order.
+__device__ __forceinline__ float sum_slots_agent(const float* base, int64_t stride, int n, const float* extra) {
+  float v = 0.0f;
+  for (int s0 = 0; s0 < n; s0 += 8) {
+    float pv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pv[j] = (s0 + j < n) ? load_agent(base + (int64_t)(s0 + j) * stride) : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (s0 + j < n) v = __fadd_rn(v, pv[j]);
+  }
+  if (extra) v = __fadd_rn(v, load_agent(extra));
+  return v;
+}
+
 }  // namespace hsmoe

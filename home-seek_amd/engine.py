@@ -114,7 +114,18 @@ class HomeSeekMoEEngine:
         tid2eid = lw.get("ffn.gate.tid2eid")
         B, T, D = hidden_states.shape
         flat = hidden_states.reshape(B * T, D)
-        if layer_idx < self.config.num_hash_layers and tid2eid is not None and input_ids is not None:
+        hashed = layer_idx < self.config.num_hash_layers and tid2eid is not None and input_ids is not None
+        if (not hashed and B * T <= ops.MAX_DECODE_TOKENS and gate_w.shape[0] <= ops.MAX_LAYER_EXPERTS
+                and flat.dtype == torch.bfloat16 and gate_w.dtype == torch.bfloat16):
+            # router + routed + shared experts in one launch (hsmoe_moe_layer_decode)
+            out, _, idx, _ = ops.moe_layer_decode(
+                flat, gate_w, gate_bias, self.store.table(layer_idx), SCALE_E8M0, self.store.shared_entry(layer_idx),
+                self.config.moe_intermediate_size, self.config.num_experts_per_tok,
+                self.config.routed_scaling_factor, self.config.swiglu_limit, out_f32=out_f32,
+                out_bf16=torch.empty(B * T, D, dtype=torch.bfloat16, device=flat.device))
+            self._last_routed_idx = idx
+            return out.reshape(B, T, D).to(hidden_states.dtype), set()
+        if hashed:
             idx, w = self._compute_hash_experts(input_ids.to(hidden_states.device), layer_idx, tid2eid)
         else:
             idx, w = self._compute_routing_experts(flat, gate_w, gate_bias)

@@ -15,10 +15,11 @@ from ._lib import SCALE_E8M0, SCALE_F32, check, lib, ptr, require_cuda, stream_p
 __all__ = [
     "SCALE_E8M0", "SCALE_F32", "scale_kind_of", "fp4_dequant_bf16", "fp8_dequant_bf16", "router_topk",
     "moe_decode", "moe_layer_decode", "moe_layer_status", "lm_head_accept", "expert_table", "shared_entry",
-    "MAX_DECODE_TOKENS",
+    "MAX_DECODE_TOKENS", "MAX_LAYER_EXPERTS",
 ]
 
 MAX_DECODE_TOKENS = 8
+MAX_LAYER_EXPERTS = 256  # expert count the one-launch layer kernel handles
 
 _workspaces: dict[tuple, torch.Tensor] = {}
 

@@ -148,8 +148,8 @@ int hsmoe_moe_down(const void* x_dev, int64_t m, int64_t d, int64_t i, const int
  * hsmoe_moe_decode; topk_idx_out int64 [m, top_k] and topk_w_out fp32
  * [m, top_k] receive the routing; logits_out bf16 [m, n_experts] or NULL;
  * out_f32 / out_bf16 as in hsmoe_moe_decode.
- * m in [1, 8], d % 512 == 0, d <= 8192, i % 512 == 0, n_experts <= 1024,
- * top_k <= 16.  The workgroups hand work to each other through the workspace;
+ * m in [1, 8], d % 512 == 0, d <= 8192, i % 512 == 0, n_experts <= 256,
+ * top_k <= 16 (larger expert counts: hsmoe_router_topk + hsmoe_moe_decode).  The workgroups hand work to each other through the workspace;
  * the launch never has more workgroups than the device holds at once.  The
  * uint32 at byte hsmoe_moe_layer_status_offset() of the workspace stays 0
  * unless a cross-workgroup wait gave up (then the outputs are not valid).
