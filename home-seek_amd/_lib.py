@@ -54,6 +54,7 @@ _SIGNATURES = {
     "hsmoe_gen_e8m0": (_int, [_u64, _i64, _int, _int, _c_void_p, _c_void_p]),
     "hsmoe_gen_normal": (_int, [_u64, _i64, _f32, _f32, _int, _c_void_p, _c_void_p]),
     "hsmoe_gen_uniform": (_int, [_u64, _i64, _f32, _f32, _f32, _c_void_p, _c_void_p]),
+    "hsmoe_gen_index": (_int, [_u64, _i64, _i64, _c_void_p, _c_void_p]),
 }
 
 _lib = None

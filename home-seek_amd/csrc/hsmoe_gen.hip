@@ -71,6 +71,14 @@ __global__ void gen_uniform_kernel(uint64_t key, int64_t n, float lo, float hi, 
   }
 }
 
+// Index uniform over [0, n_values): ((r >> 32) * n_values) >> 32.
+__global__ void gen_index_kernel(uint64_t key, int64_t n, uint32_t n_values, int64_t* __restrict__ out) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const uint64_t r = rand64(key, (uint64_t)i);
+    out[i] = (int64_t)(((r >> 32) * (uint64_t)n_values) >> 32);
+  }
+}
+
 }  // namespace
 }  // namespace hsmoe
 
@@ -123,4 +131,13 @@ extern "C" int hsmoe_gen_uniform(uint64_t key, int64_t n, float lo, float hi, fl
   hipLaunchKernelGGL(gen_uniform_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, (hipStream_t)stream, key, n, lo, hi,
                      mul, out);
   return check_launch("hsmoe_gen_uniform");
+}
+
+extern "C" int hsmoe_gen_index(uint64_t key, int64_t n, int64_t n_values, int64_t* out, hsmoe_stream_t stream) {
+  if (n < 0 || (n > 0 && !out) || n_values < 1 || n_values > 0xffffffffll)
+    return fail(HSMOE_ERR_ARG, "hsmoe_gen_index: bad arguments");
+  if (n == 0) return HSMOE_OK;
+  hipLaunchKernelGGL(gen_index_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, (hipStream_t)stream, key, n,
+                     (uint32_t)n_values, out);
+  return check_launch("hsmoe_gen_index");
 }

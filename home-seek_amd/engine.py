@@ -9,6 +9,8 @@ and MTP loop can call them unchanged:
   _get_shared_expert                              engine.py:1779-1849
   _forward_ffn                                    engine.py:1410-1541
   _mtp_verify_batched                             engine.py:2431-2540
+  _mtp_generate_draft (stand-in, see below)        engine.py:2251-2339
+  decode_step / generate_greedy                    engine.py:2809-2922 (temperature 0)
 Attention, mHC, KV caches and sampling stay with the host engine; the hooks
 `_snapshot_verify_state` / `_restore_verify_state` are where a full engine
 saves and trims its attention state around a verify (no-ops here).
@@ -18,7 +20,14 @@ Divergences from the reference, all deliberate:
     (the reference's BF16 cache is keyed by (eid, device) and aliases expert
     e of the first layer that loaded it, engine.py:1319-1323).
   * no host synchronisation inside _forward_ffn (the reference calls .tolist()
-    on the routing ids, engine.py:1432-1433); _mtp_verify_batched syncs once.
+    on the routing ids, engine.py:1432-1433); _mtp_verify_batched syncs once,
+    decode_step not at all (the acceptance outcome stays on the device).
+  * the MTP draft module keeps the reference's data flow (hnorm of the main
+    model's last hidden state + enorm of the token embedding, one MoE block
+    with the MTP experts, the MTP norm, lm_head, greedy argmax; second draft
+    from the first) without its attention and without the e_proj / h_proj
+    projections, which are outside the MoE path; its experts are one more
+    layer of the HBM store (the checkpoint's mtp.0.ffn.experts.*).
 """
 from __future__ import annotations
 
@@ -35,8 +44,11 @@ from .router import compute_expert_affinity_with_bias
 class HomeSeekMoEEngine:
     def __init__(self, config: MoEConfig, store: HbmExpertStore, layer_weights: dict[int, dict],
                  lm_head: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None,
-                 embed: torch.Tensor | None = None):
+                 embed: torch.Tensor | None = None, mtp_weights: dict | None = None):
         self.config = config
+        # mtp_weights: {"hnorm.weight", "enorm.weight", "norm.weight", "layer": layer
+        # weights of the MTP block (as for _forward_layer), "layer_idx": its store layer}
+        self._mtp_weights = mtp_weights
         self.store = store
         self.device = store.device
         self._layer_weights = layer_weights
@@ -178,12 +190,78 @@ class HomeSeekMoEEngine:
             self._restore_verify_state(snap, n_accept, t_total)
         return n_accept, bonus_logits
 
-    # ------------------------------------------------------------ layer stand-in
     def _embed(self, ids: torch.Tensor) -> torch.Tensor:
         if self.embed is None:
             raise RuntimeError("no embedding table: pass embed= or override _embed")
         return self.embed[ids].to(torch.bfloat16)
 
+    # ------------------------------------------------------------ MTP draft + decode loop
+    @torch.no_grad()
+    def _mtp_generate_draft(self, last_hidden: torch.Tensor, num_draft: int = 2, temperature: float = 0.0,
+                            last_token_id: torch.Tensor | None = None):
+        """Greedy drafts from the MTP block (engine.py:2251-2339, stand-in described
+        in the module docstring) -> (draft_ids [1, n] int64, n); no host sync."""
+        mw = self._mtp_weights
+        if mw is None or self.embed is None or self.lm_head is None or last_token_id is None:
+            return None, 0
+        eps = self.config.rms_norm_eps
+        D = last_hidden.shape[-1]
+        h_prev = last_hidden.reshape(1, 1, D)
+        tok = last_token_id.reshape(1, 1)
+        drafts = []
+        for _ in range(num_draft):
+            e = rms_norm(self._embed(tok).reshape(1, D), mw["enorm.weight"], eps)
+            h_in = rms_norm(h_prev.reshape(1, D), mw["hnorm.weight"], eps) + e
+            h_prev, _ = self._forward_layer(h_in.reshape(1, 1, D), mw["layer"], mw["layer_idx"], tok)
+            hf = rms_norm(h_prev.reshape(1, D), mw["norm.weight"], eps)
+            _, pred, _ = ops.lm_head_accept(hf, self.lm_head, None, want_logits=False)
+            tok = pred.reshape(1, 1)
+            drafts.append(tok)
+        return torch.cat(drafts, dim=-1), num_draft
+
+    def _forward_stack(self, ids: torch.Tensor) -> torch.Tensor:
+        """Embed ids [1, T] and run every layer -> last hidden [1, T, D]."""
+        h = self._embed(ids)
+        for layer_idx in range(self.config.num_hidden_layers):
+            h, _ = self._forward_layer(h, self._get_layer_weights(layer_idx), layer_idx, ids)
+        return h
+
+    @torch.no_grad()
+    def decode_step(self, cur: torch.Tensor, out_row: torch.Tensor | None = None):
+        """One greedy decode step with MTP verify, on the device only
+        (engine.py:2809-2922 at temperature 0): M=1 forward of `cur` -> main
+        token A; drafts [d0, d1]; verify [A, d0, d1]; n = accepted drafts.
+        Returns (row [4] = A, d0, d1, bonus token; count of tokens emitted =
+        1 + (n > 0) * (n + 1); next token to forward; n), all device tensors."""
+        cur = cur.reshape(1, 1)
+        h = self._forward_stack(cur)
+        _, pred, _ = ops.lm_head_accept(self._final_hidden(h), self.lm_head, None, want_logits=False)
+        a = pred.reshape(1, 1)
+        drafts, n_draft = self._mtp_generate_draft(h, self.config.mtp_num_draft, 0.0, last_token_id=a)
+        combined = torch.cat([a, drafts], dim=-1)
+        hv = self._forward_stack(combined)
+        _, pred_v, result = ops.lm_head_accept(self._final_hidden(hv), self.lm_head, combined.reshape(-1),
+                                               want_logits=False)
+        n_acc = result[0]
+        bonus = pred_v.index_select(0, result[1:2]).reshape(())  # no host read of the row
+        row = torch.cat([a.reshape(1), drafts.reshape(-1), bonus.reshape(1)])
+        if out_row is not None:
+            out_row.copy_(row)
+        count = 1 + (n_acc > 0).to(torch.int64) * (n_acc + 1)
+        nxt = torch.where(n_acc > 0, bonus, a.reshape(()))
+        return row, count, nxt, n_acc
+
+    @torch.no_grad()
+    def generate_greedy(self, first_id: int, steps: int, graph: bool = True):
+        """`steps` decode steps from token first_id -> (tokens list, accepted
+        drafts per step).  With graph=True one step is captured as a HIP graph
+        and replayed: no host synchronisation until the end."""
+        dec = GreedyDecoder(self, steps, graph)
+        dec.reset(first_id)
+        dec.run(steps)
+        return dec.result()
+
+    # ------------------------------------------------------------ layer stand-in
     def _forward_layer(self, h: torch.Tensor, lw: dict, layer_idx: int, input_ids=None):
         """Layer with attention replaced by a fixed residual lw["attn.residual"] [D]:
         h = h + r; h = h + FFN(rms_norm(h, ffn_norm))  (engine.py:2653-2690 without mHC)."""
@@ -196,6 +274,75 @@ class HomeSeekMoEEngine:
             hn = rms_norm(h.reshape(-1, h.shape[-1]), norm_w, self.config.rms_norm_eps).reshape(h.shape)
         ffn_out, used = self._forward_ffn(hn, lw, layer_idx, input_ids)
         return h + ffn_out, used
+
+
+class GreedyDecoder:
+    """Device-resident greedy decode loop with MTP verify (engine.py:2809-2922 at
+    temperature 0).  Per step it records the row [A, d0, d1, bonus], the count of
+    tokens emitted and the accepted drafts into device buffers of `capacity`
+    steps, and carries the next token on the device; with graph=True one step
+    is captured as a HIP graph (after one eager warm-up step, so that every
+    workspace exists before capture) and replayed."""
+
+    def __init__(self, engine: HomeSeekMoEEngine, capacity: int, graph: bool = True):
+        dev = engine.device
+        if capacity < 1:
+            raise ValueError("a decoder needs room for at least one step")
+        self.engine, self.capacity = engine, int(capacity)
+        self.rows = torch.zeros(self.capacity, 4, dtype=torch.int64, device=dev)
+        self.counts = torch.zeros(self.capacity, dtype=torch.int64, device=dev)
+        self.n_accs = torch.zeros(self.capacity, dtype=torch.int64, device=dev)
+        self.cur = torch.zeros(1, 1, dtype=torch.int64, device=dev)
+        self.k = torch.zeros((), dtype=torch.int64, device=dev)  # next row, on the device
+        self.done = 0  # rows written, on the host (bounds every run)
+        self.graph = None
+        if graph:
+            stream = torch.cuda.Stream(device=dev)
+            stream.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(stream):
+                self._body()  # warm-up step into row 0, overwritten after reset()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=stream):
+                    self._body()
+            torch.cuda.current_stream(dev).wait_stream(stream)
+            self.graph = g
+
+    def _body(self):
+        row, count, nxt, n_acc = self.engine.decode_step(self.cur)
+        at = self.k.reshape(1)
+        self.rows.index_copy_(0, at, row.reshape(1, 4))
+        self.counts.index_copy_(0, at, count.reshape(1))
+        self.n_accs.index_copy_(0, at, n_acc.reshape(1))
+        self.cur.copy_(nxt.reshape(1, 1))
+        self.k.add_(1)
+
+    def reset(self, first_id: int | None = None) -> None:
+        """Rewinds the row index; first_id (if given) becomes the token to forward."""
+        if first_id is not None:
+            self.cur.fill_(int(first_id))
+        self.k.zero_()
+        self.done = 0
+
+    def run(self, n: int) -> None:
+        if self.done + n > self.capacity:
+            raise ValueError(f"{n} more steps exceed the decoder's capacity of {self.capacity} rows")
+        for _ in range(n):
+            if self.graph is not None:
+                self.graph.replay()
+            else:
+                self._body()
+        self.done += n
+
+    def result(self):
+        """(tokens emitted, accepted drafts per step) of the rows written since reset()."""
+        n = self.done
+        rows_h, counts_h = self.rows[:n].cpu().tolist(), self.counts[:n].cpu().tolist()
+        tokens = []
+        for r, c in zip(rows_h, counts_h):
+            tokens.append(r[0])
+            if c > 1:
+                tokens.extend(r[1:c - 1] + [r[3]])
+        return tokens, self.n_accs[:n].cpu().tolist()
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:

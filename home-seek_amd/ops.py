@@ -313,6 +313,14 @@ def gen_uniform(key: int, out: torch.Tensor, lo: float, hi: float, mul: float = 
     return out
 
 
+def gen_index(key: int, out: torch.Tensor, n_values: int) -> torch.Tensor:
+    dev = require_cuda(out)
+    if out.dtype != torch.int64:
+        raise TypeError("gen_index fills int64 tensors")
+    check(lib().hsmoe_gen_index(key, out.numel(), n_values, ptr(out), stream_ptr(dev)), "hsmoe_gen_index")
+    return out
+
+
 def key(seed: int, tag: int) -> int:
     """Stream key = splitmix64 output number tag+1 for `seed` (same as the device's rand64)."""
     from .synthetic import rand64

@@ -203,6 +203,8 @@ int hsmoe_gen_normal(uint64_t key, int64_t n, float mean, float std, int as_bf16
                      hsmoe_stream_t stream);
 int hsmoe_gen_uniform(uint64_t key, int64_t n, float lo, float hi, float mul, float* out_dev,
                       hsmoe_stream_t stream);
+/* int64 index uniform over [0, n_values): ((r >> 32) * n_values) >> 32. */
+int hsmoe_gen_index(uint64_t key, int64_t n, int64_t n_values, int64_t* out_dev, hsmoe_stream_t stream);
 
 #ifdef __cplusplus
 }

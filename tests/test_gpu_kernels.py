@@ -50,7 +50,7 @@ def test_fp8_dequant_all_codes(dev):
     assert bf16_same(orc.to_np_bf16(got), orc.dequant_fp8(data, sf))
 
 
-@pytest.mark.parametrize("kind", ["bytes", "e4m3", "e8m0", "normal_bf16", "normal_f32", "uniform"])
+@pytest.mark.parametrize("kind", ["bytes", "e4m3", "e8m0", "normal_bf16", "normal_f32", "uniform", "index"])
 def test_generators_match_host(dev, kind):
     k = orc.key(99, orc.tag(5, 1, 2, 3))
     n = 100003
@@ -67,6 +67,9 @@ def test_generators_match_host(dev, kind):
     elif kind == "normal_f32":
         t = ops.gen_normal(k, torch.empty(n, dtype=torch.float32, device=dev), 1.0, 0.05)
         ref = orc.gen_normal_f32(k, n, 1.0, 0.05)
+    elif kind == "index":
+        t = ops.gen_index(k, torch.empty(n, dtype=torch.int64, device=dev), 129280)
+        ref = orc.gen_index(k, n, 129280)
     else:
         t = ops.gen_uniform(k, torch.empty(n, dtype=torch.float32, device=dev), 0.5, 2.0, 1.0 / 448.0)
         ref = orc.gen_uniform_f32(k, n, 0.5, 2.0, np.float32(1.0 / 448.0))

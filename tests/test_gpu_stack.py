@@ -1,0 +1,173 @@
+"""GPU parity of the MoE-only decode stack (layers, MTP drafts, verify, decode loop)
+against the CPU stack oracle, at a small shape the oracle runs in seconds.
+
+Per layer the device is teacher-forced: the oracle recomputes each layer from
+the device's own input, so errors do not compound.  Bars: the residual add is
+bit-exact (a bf16 add), RMSNorm within one bf16 step, router and hash expert
+ids bit-exact, the FFN within max-abs 2e-2 / rel-L2 1e-3 of the fp32 oracle.
+
+Token streams: with attention replaced by a fixed residual the next token is a
+function f of the current one, so a greedy stream with MTP verify must equal
+the plain chain f(f(...f(first))) whatever the drafts are (speculative
+decoding only changes how many tokens a step emits).  That invariant is
+checked with the MTP block's drafts, with perfect drafts (every step accepts
+both), with a half-right draft (accepts one) and with wrong drafts (accepts
+none), and the free-running stream is compared with the oracle's.
+"""
+import numpy as np
+import pytest
+import torch
+
+from home_seek_amd import ops, stack
+from oracle import oracle as orc
+from oracle.stack import StackOracle
+
+pytestmark = pytest.mark.gpu
+
+SEED, NL, E, D, I, V, K, NH = 4242, 4, 16, 512, 512, 1024, 6, 1
+
+
+@pytest.fixture(scope="module")
+def model(dev):
+    eng = stack.build_stack(SEED, n_layers=NL, n_experts=E, d=D, i=I, vocab=V, top_k=K, n_hash=NH, device=dev)
+    torch.cuda.synchronize()
+    return eng, StackOracle(SEED, NL, E, D, I, V, K, NH)
+
+
+def np16(t: torch.Tensor) -> np.ndarray:
+    return orc.to_np_bf16(t.reshape(-1, t.shape[-1]))
+
+
+def within_one_step(got: np.ndarray, ref: np.ndarray) -> bool:
+    g, r = orc.bf16_to_f32(got), orc.bf16_to_f32(ref)
+    return bool(np.all(np.abs(g - r) <= np.abs(r) * 2.0 ** -7))
+
+
+def check_ffn(got: np.ndarray, ref: np.ndarray, what: str):
+    err = got.astype(np.float64) - ref.astype(np.float64)
+    rel = np.linalg.norm(err) / np.linalg.norm(ref)
+    mx = np.abs(err).max()
+    print(f"[{what}] rel-L2 {rel:.3e} max-abs {mx:.3e}")
+    assert rel <= 1e-3 and mx <= 2e-2, (what, rel, mx)
+
+
+def device_next(eng, ids: torch.Tensor) -> torch.Tensor:
+    """Greedy next token of each id in ids [1, T] (plain forward, no MTP) -> [T] int64."""
+    h = eng._forward_stack(ids.reshape(1, -1))
+    _, pred, _ = ops.lm_head_accept(eng._final_hidden(h), eng.lm_head, None, want_logits=False)
+    return pred
+
+
+def test_synthetic_weights_match_oracle(model):
+    eng, so = model
+    lw = eng._get_layer_weights(0)
+    assert np.array_equal(np16(lw["ffn.gate.weight"]), so.layers[0]["gate"])
+    assert np.array_equal(lw["ffn.gate.tid2eid"].cpu().numpy(), so.layers[0]["tid2eid"])
+    assert np.array_equal(np16(eng.lm_head), so.lm_head)
+    for l in range(NL):
+        assert np.array_equal(np16(eng._get_layer_weights(l)["attn.residual"])[0], so.layers[l]["residual"])
+    # hash ids of one token are distinct (odd step, power-of-two E)
+    t = so.layers[0]["tid2eid"]
+    assert all(len(set(r)) == K for r in t.tolist())
+
+
+@pytest.mark.parametrize("ids", [[7], [3, 900, 3], [1023, 0, 512]])
+def test_layers_match_oracle_teacher_forced(model, ids):
+    eng, so = model
+    tid = torch.tensor([ids], dtype=torch.int64, device=eng.device)
+    h = eng._embed(tid)
+    assert np.array_equal(np16(h), so.embed(ids))
+    for l in range(NL):
+        lw = eng._get_layer_weights(l)
+        ref = so.layer(np16(h), so.layers[l], l, ids)
+        h1 = h + lw["attn.residual"]
+        assert np.array_equal(np16(h1), ref["h1"]), l
+        hn = ops.rms_norm(h1.reshape(-1, D), lw["ffn_norm.weight"]).reshape(h1.shape)
+        assert within_one_step(np16(hn), ref["hn"]), l
+        f32 = torch.empty(len(ids), D, dtype=torch.float32, device=eng.device)
+        ffn, _ = eng._forward_ffn(hn, lw, l, tid, out_f32=f32)
+        # the FFN from the device's own normed input
+        f_ref, idx_ref = so.ffn(np16(hn), so.layers[l], l, ids)
+        assert np.array_equal(eng._last_routed_idx.reshape(len(ids), K).cpu().numpy(), idx_ref), l
+        check_ffn(f32.cpu().numpy(), f_ref, f"layer {l} T={len(ids)}")
+        assert np.array_equal(np16(ffn), orc.f32_to_bf16(f32.cpu().numpy()))
+        h_next, _ = eng._forward_layer(h, lw, l, tid)
+        assert np.array_equal(np16(h_next), np16(h1 + ffn)), l
+        h = h_next
+
+
+def test_verify_rows_equal_single_token_forwards(model):
+    """No attention: row t of a T=3 verify is the M=1 forward of token t, bit for bit."""
+    eng, _ = model
+    ids = torch.tensor([[5, 77, 5]], dtype=torch.int64, device=eng.device)
+    h3 = eng._forward_stack(ids)
+    for t in range(3):
+        h1 = eng._forward_stack(ids[:, t:t + 1])
+        assert torch.equal(h3[0, t], h1[0, 0]), t
+
+
+def test_mtp_drafts_match_oracle(model):
+    eng, so = model
+    cur = torch.tensor([[42]], dtype=torch.int64, device=eng.device)
+    h = eng._forward_stack(cur)
+    a = device_next(eng, cur).reshape(1, 1)
+    drafts, n = eng._mtp_generate_draft(h, 2, 0.0, last_token_id=a)
+    assert n == 2 and tuple(drafts.shape) == (1, 2)
+    assert a.item() == so.next_token(42)
+    assert drafts.cpu().tolist()[0] == so.drafts(np16(h), a.item(), 2)
+
+
+def chain(first: int, n: int, f) -> list:
+    out, t = [], first
+    for _ in range(n):
+        t = f(t)
+        out.append(t)
+    return out
+
+
+def test_decode_stream_matches_oracle_and_greedy_chain(model):
+    eng, so = model
+    steps = 5
+    tokens, accs = eng.generate_greedy(11, steps, graph=False)
+    margins = []
+    ref_tokens, ref_accs = so.generate(11, steps, margins)
+    print(f"tokens {tokens} accepted {accs}; smallest oracle top-2 logit gap {min(margins):.3e}")
+    assert tokens == ref_tokens and accs == ref_accs
+    assert all(0 <= a <= 2 for a in accs) and len(tokens) == steps + sum(a + 1 for a in accs if a > 0)
+    f = lambda t: device_next(eng, torch.tensor([[t]], device=eng.device)).item()
+    assert tokens == chain(11, len(tokens), f)
+
+
+@pytest.mark.parametrize("kind,want", [("perfect", 2), ("half", 1), ("wrong", 0)])
+def test_acceptance_paths_keep_the_greedy_chain(model, kind, want):
+    eng, so = model
+
+    def drafts_on_device(last_hidden, num_draft=2, temperature=0.0, last_token_id=None):
+        d0 = device_next(eng, last_token_id.reshape(1, 1)).reshape(1, 1)
+        d1 = device_next(eng, d0).reshape(1, 1)
+        if kind == "half":
+            d1 = (d1 + 1) % V
+        elif kind == "wrong":
+            d0 = (d0 + 1) % V
+        return torch.cat([d0, d1], dim=-1), 2
+
+    def drafts_oracle(h, a):
+        d0 = so.next_token(a)
+        d1 = so.next_token(d0)
+        return [d0, (d1 + 1) % V] if kind == "half" else [(d0 + 1) % V, d1] if kind == "wrong" else [d0, d1]
+
+    eng._mtp_generate_draft = drafts_on_device
+    try:
+        tokens, accs = eng.generate_greedy(300, 3, graph=False)
+    finally:
+        del eng._mtp_generate_draft
+    assert accs == [want] * 3
+    assert (tokens, accs) == so.generate(300, 3, draft_fn=drafts_oracle)
+    assert tokens == chain(300, len(tokens), so.next_token)
+
+
+def test_graph_replays_equal_eager(model):
+    eng, _ = model
+    eager = eng.generate_greedy(600, 6, graph=False)
+    for _ in range(2):
+        assert eng.generate_greedy(600, 6, graph=True) == eager
