@@ -49,6 +49,8 @@ _SIGNATURES = {
     "hsmoe_lm_head_accept": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
                                     _c_void_p, _c_void_p, _size, _c_void_p]),
     "hsmoe_rms_norm": (_int, [_c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p, _c_void_p]),
+    "hsmoe_add_rms_norm": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p,
+                                  _c_void_p, _c_void_p]),
     "hsmoe_gen_bytes": (_int, [_u64, _i64, _c_void_p, _c_void_p]),
     "hsmoe_gen_e4m3": (_int, [_u64, _i64, _c_void_p, _c_void_p]),
     "hsmoe_gen_e8m0": (_int, [_u64, _i64, _int, _int, _c_void_p, _c_void_p]),

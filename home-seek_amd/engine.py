@@ -178,10 +178,7 @@ class HomeSeekMoEEngine:
         try:
             self._global_pos = pos_bak + 1
             self._phase = "verify"
-            h = self._embed(combined)
-            for layer_idx in range(self.config.num_hidden_layers):
-                h, _ = self._forward_layer(h, self._get_layer_weights(layer_idx), layer_idx, combined)
-            hf = self._final_hidden(h)
+            _, hf = self._forward_stack(combined)
             logits, pred, result = ops.lm_head_accept(hf, self.lm_head, combined.reshape(-1))
             n_accept, bonus_row = (int(v) for v in result.tolist())  # the one host sync per verify
             bonus_logits = logits[bonus_row:bonus_row + 1]
@@ -219,12 +216,31 @@ class HomeSeekMoEEngine:
             drafts.append(tok)
         return torch.cat(drafts, dim=-1), num_draft
 
-    def _forward_stack(self, ids: torch.Tensor) -> torch.Tensor:
-        """Embed ids [1, T] and run every layer -> last hidden [1, T, D]."""
+    def _forward_stack(self, ids: torch.Tensor, final_norm: bool = True):
+        """Embed ids [1, T] and run every layer -> (last hidden [1, T, D], its
+        final RMSNorm [T, D] or None).  Same values as _forward_layer in a loop;
+        each layer's FFN output is added in the next layer's fused add + norm
+        launch (hsmoe_add_rms_norm), which also adds that layer's residual."""
+        eps = self.config.rms_norm_eps
         h = self._embed(ids)
+        pending = None  # FFN output of the previous layer, not yet added
         for layer_idx in range(self.config.num_hidden_layers):
-            h, _ = self._forward_layer(h, self._get_layer_weights(layer_idx), layer_idx, ids)
-        return h
+            lw = self._get_layer_weights(layer_idx)
+            norm_w = lw.get("ffn_norm.weight")
+            if norm_w is None:
+                if pending is not None:
+                    h, pending = h + pending, None
+                h, _ = self._forward_layer(h, lw, layer_idx, ids)
+                continue
+            h, hn = ops.add_rms_norm(h, norm_w, add=pending, residual=lw.get("attn.residual"), eps=eps,
+                                     want_sum=True)
+            pending, _ = self._forward_ffn(hn, lw, layer_idx, ids)
+        if final_norm and self.norm_weight is not None:
+            h, hf = ops.add_rms_norm(h, self.norm_weight, add=pending, eps=eps, want_sum=True)
+            return h, hf.reshape(-1, h.shape[-1])
+        if pending is not None:
+            h = h + pending
+        return h, (self._final_hidden(h) if final_norm else None)
 
     @torch.no_grad()
     def decode_step(self, cur: torch.Tensor, out_row: torch.Tensor | None = None):
@@ -234,14 +250,13 @@ class HomeSeekMoEEngine:
         Returns (row [4] = A, d0, d1, bonus token; count of tokens emitted =
         1 + (n > 0) * (n + 1); next token to forward; n), all device tensors."""
         cur = cur.reshape(1, 1)
-        h = self._forward_stack(cur)
-        _, pred, _ = ops.lm_head_accept(self._final_hidden(h), self.lm_head, None, want_logits=False)
+        h, hf = self._forward_stack(cur)
+        _, pred, _ = ops.lm_head_accept(hf, self.lm_head, None, want_logits=False)
         a = pred.reshape(1, 1)
         drafts, n_draft = self._mtp_generate_draft(h, self.config.mtp_num_draft, 0.0, last_token_id=a)
         combined = torch.cat([a, drafts], dim=-1)
-        hv = self._forward_stack(combined)
-        _, pred_v, result = ops.lm_head_accept(self._final_hidden(hv), self.lm_head, combined.reshape(-1),
-                                               want_logits=False)
+        _, hfv = self._forward_stack(combined)
+        _, pred_v, result = ops.lm_head_accept(hfv, self.lm_head, combined.reshape(-1), want_logits=False)
         n_acc = result[0]
         bonus = pred_v.index_select(0, result[1:2]).reshape(())  # no host read of the row
         row = torch.cat([a.reshape(1), drafts.reshape(-1), bonus.reshape(1)])
@@ -266,12 +281,13 @@ class HomeSeekMoEEngine:
         """Layer with attention replaced by a fixed residual lw["attn.residual"] [D]:
         h = h + r; h = h + FFN(rms_norm(h, ffn_norm))  (engine.py:2653-2690 without mHC)."""
         r = lw.get("attn.residual")
-        if r is not None:
-            h = h + r
-        hn = h
         norm_w = lw.get("ffn_norm.weight")
         if norm_w is not None:
-            hn = rms_norm(h.reshape(-1, h.shape[-1]), norm_w, self.config.rms_norm_eps).reshape(h.shape)
+            h, hn = ops.add_rms_norm(h, norm_w, residual=r, eps=self.config.rms_norm_eps, want_sum=True)
+        else:
+            if r is not None:
+                h = h + r
+            hn = h
         ffn_out, used = self._forward_ffn(hn, lw, layer_idx, input_ids)
         return h + ffn_out, used
 

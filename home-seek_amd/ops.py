@@ -269,16 +269,35 @@ def lm_head_accept(h: torch.Tensor, lm_head: torch.Tensor, ids: torch.Tensor | N
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """bf16 RMSNorm over the last dimension (utils.py:6-9)."""
-    dev = require_cuda(x, weight)
-    if x.dtype != torch.bfloat16:
-        raise TypeError("rms_norm takes bf16 input")
+    return add_rms_norm(x, weight, eps=eps)[1]
+
+
+def add_rms_norm(x: torch.Tensor, weight: torch.Tensor, add: torch.Tensor | None = None,
+                 residual: torch.Tensor | None = None, eps: float = 1e-6, want_sum: bool = False):
+    """h = x (+ add) (+ residual), as torch bf16 adds; -> (h if want_sum else None, RMSNorm(h)).
+    x, add: [..., D] bf16 of one shape; residual: [D] bf16, added to every row."""
+    dev = require_cuda(x, weight, add, residual)
+    if x.dtype != torch.bfloat16 or (add is not None and add.dtype != torch.bfloat16):
+        raise TypeError("add_rms_norm takes bf16 rows")
     shape = x.shape
-    x2 = x.reshape(-1, shape[-1]).contiguous()
-    w = weight.to(torch.bfloat16).contiguous()
+    d = shape[-1]
+    x2 = x.reshape(-1, d).contiguous()
+    if add is not None:
+        if add.shape != shape:
+            raise ValueError(f"add {tuple(add.shape)} does not match x {tuple(shape)}")
+        add = add.reshape(-1, d).contiguous()
+    if residual is not None:
+        residual = residual.to(torch.bfloat16).reshape(-1).contiguous()
+        if residual.numel() != d:
+            raise ValueError("residual must be one row of the hidden size")
+    w = weight.to(torch.bfloat16).reshape(-1).contiguous()
+    if w.numel() != d:
+        raise ValueError("norm weight must be one row of the hidden size")
     out = torch.empty_like(x2)
-    check(lib().hsmoe_rms_norm(ptr(x2), ptr(w), x2.shape[0], x2.shape[1], eps, ptr(out), stream_ptr(dev)),
-          "hsmoe_rms_norm")
-    return out.reshape(shape)
+    h = torch.empty_like(x2) if want_sum else None
+    check(lib().hsmoe_add_rms_norm(ptr(x2), ptr(add), ptr(residual), ptr(w), x2.shape[0], d, eps, ptr(h), ptr(out),
+                                   stream_ptr(dev)), "hsmoe_add_rms_norm")
+    return (None if h is None else h.reshape(shape)), out.reshape(shape)
 
 
 # ---------------------------------------------------------------- generators

@@ -190,6 +190,16 @@ int hsmoe_lm_head_accept(const void* h_dev, const void* lm_head_dev, int64_t n_t
 int hsmoe_rms_norm(const void* x_dev, const void* w_dev, int64_t rows, int64_t d, float eps, void* out_dev,
                    hsmoe_stream_t stream);
 
+/* The residual adds of a layer fused in front of its RMSNorm (reference
+ * engine.py:2653-2690, the attention output and the FFN output added to the
+ * residual stream, as torch bf16 adds: fp32 sum rounded once):
+ *   h = x; if add: h = bf16(h + add[r]); if res: h = bf16(h + res)   (res is one [d] row)
+ *   h_out[r] = h (if h_out); out[r] = RMSNorm(h) as hsmoe_rms_norm.
+ * d must be a multiple of 8 (<= 16384); all rows 16-byte aligned.  hsmoe_rms_norm
+ * is this entry point with add = res = h_out = NULL. */
+int hsmoe_add_rms_norm(const void* x_dev, const void* add_dev, const void* res_dev, const void* w_dev, int64_t rows,
+                       int64_t d, float eps, void* h_out_dev, void* out_dev, hsmoe_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Synthetic data generators (counter-based, reproducible on the host): value i
  * of a stream is derived from r = splitmix64 output number i+1 for seed `key`.

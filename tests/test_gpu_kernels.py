@@ -141,3 +141,22 @@ def test_rms_norm_within_one_ulp(dev):
     ulp = np.abs(ref) * 2.0 ** -7
     assert np.all(np.abs(got - ref) <= ulp)
     assert np.mean(got == ref) > 0.98
+
+
+@pytest.mark.parametrize("rows,d", [(1, 4096), (3, 4096), (5, 512), (2, 16384)])
+def test_add_rms_norm_matches_torch_adds_and_oracle(dev, rows, d):
+    """h = bf16(bf16(x + add) + res) bit-exact against torch's bf16 adds; the norm
+    within one bf16 step of the oracle (and equal to hsmoe_rms_norm of h)."""
+    seed = 11 + rows
+    x = synthetic.hidden(seed, 1, rows, d, dev)
+    add = synthetic.hidden(seed, 2, rows, d, dev)
+    res = synthetic.normal_bf16(seed, synthetic.tag(synthetic.KIND_RESIDUAL), (d,), 0.0, 0.1, dev)
+    w = synthetic.normal_bf16(seed, synthetic.tag(synthetic.KIND_NORM_W), (d,), 1.0, 0.05, dev)
+    h, hn = ops.add_rms_norm(x, w, add=add, residual=res, want_sum=True)
+    assert torch.equal(h, (x + add) + res)
+    assert torch.equal(hn, ops.rms_norm(h, w))
+    got = orc.bf16_to_f32(orc.to_np_bf16(hn))
+    ref = orc.bf16_to_f32(orc.rms_norm(orc.to_np_bf16(h), orc.to_np_bf16(w)))
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7)
+    h2, hn2 = ops.add_rms_norm(x, w, residual=res, want_sum=True)
+    assert torch.equal(h2, x + res) and torch.equal(hn2, ops.rms_norm(x + res, w))

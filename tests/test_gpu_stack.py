@@ -53,8 +53,8 @@ def check_ffn(got: np.ndarray, ref: np.ndarray, what: str):
 
 def device_next(eng, ids: torch.Tensor) -> torch.Tensor:
     """Greedy next token of each id in ids [1, T] (plain forward, no MTP) -> [T] int64."""
-    h = eng._forward_stack(ids.reshape(1, -1))
-    _, pred, _ = ops.lm_head_accept(eng._final_hidden(h), eng.lm_head, None, want_logits=False)
+    _, hf = eng._forward_stack(ids.reshape(1, -1))
+    _, pred, _ = ops.lm_head_accept(hf, eng.lm_head, None, want_logits=False)
     return pred
 
 
@@ -100,16 +100,28 @@ def test_verify_rows_equal_single_token_forwards(model):
     """No attention: row t of a T=3 verify is the M=1 forward of token t, bit for bit."""
     eng, _ = model
     ids = torch.tensor([[5, 77, 5]], dtype=torch.int64, device=eng.device)
-    h3 = eng._forward_stack(ids)
+    h3, f3 = eng._forward_stack(ids)
     for t in range(3):
-        h1 = eng._forward_stack(ids[:, t:t + 1])
-        assert torch.equal(h3[0, t], h1[0, 0]), t
+        h1, f1 = eng._forward_stack(ids[:, t:t + 1])
+        assert torch.equal(h3[0, t], h1[0, 0]) and torch.equal(f3[t], f1[0]), t
+
+
+def test_fused_stack_equals_layer_loop(model):
+    """The fused add + norm chain gives the values of the plain layer loop, bit for bit."""
+    eng, _ = model
+    ids = torch.tensor([[9, 400, 1000]], dtype=torch.int64, device=eng.device)
+    h = eng._embed(ids)
+    for l in range(NL):
+        h, _ = eng._forward_layer(h, eng._get_layer_weights(l), l, ids)
+    hf = eng._final_hidden(h)
+    h2, hf2 = eng._forward_stack(ids)
+    assert torch.equal(h, h2) and torch.equal(hf, hf2)
 
 
 def test_mtp_drafts_match_oracle(model):
     eng, so = model
     cur = torch.tensor([[42]], dtype=torch.int64, device=eng.device)
-    h = eng._forward_stack(cur)
+    h, _ = eng._forward_stack(cur)
     a = device_next(eng, cur).reshape(1, 1)
     drafts, n = eng._mtp_generate_draft(h, 2, 0.0, last_token_id=a)
     assert n == 2 and tuple(drafts.shape) == (1, 2)
