@@ -49,9 +49,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="default 400 (layer) / 64 (stack)")
     ap.add_argument("--warmup", type=int, default=None, help="default 40 (layer) / 4 (stack)")
-    ap.add_argument("--workload", choices=("layer", "stack"), default="layer",
+    ap.add_argument("--workload", choices=("layer", "stack", "prefill"), default="layer",
                     help="layer: one MoE layer at decode M=1 (+ M=3 and lm_head side measurements); "
-                         "stack: the 43-layer MoE-only decode loop with MTP verify, tok/s")
+                         "stack: the 43-layer MoE-only decode loop with MTP verify, tok/s; "
+                         "prefill: the M=512 grouped GEMM over Zipf(1.1)-routed experts")
     ap.add_argument("--stack-layers", type=int, default=43)
     ap.add_argument("--layers", type=int, default=8, help="distinct layers rotated through (MALL defeat)")
     ap.add_argument("--seed", type=int, default=1234)
@@ -66,9 +67,9 @@ def parse():
     args = ap.parse_args()
     stack = args.workload == "stack"
     if args.steps is None:
-        args.steps = 64 if stack else 400
+        args.steps = {"stack": 64, "prefill": 50}.get(args.workload, 400)
     if args.warmup is None:
-        args.warmup = 4 if stack else 40
+        args.warmup = {"stack": 4, "prefill": 5}.get(args.workload, 40)
     return args
 
 
@@ -80,8 +81,8 @@ def main():
         sys.exit(2)
     import torch
     __graft_entry__.package()
-    if args.workload == "stack":
-        print(json.dumps(run_stack(args, torch)))
+    if args.workload in ("stack", "prefill"):
+        print(json.dumps((run_stack if args.workload == "stack" else run_prefill)(args, torch)))
         return
     from home_seek_amd import expert_store, ops, synthetic
 
@@ -406,6 +407,90 @@ def run_stack(args, torch):
                      "lm_head_bytes_per_step": lm_bytes // args.steps},
         "build_s": round(t_build, 1),
         "wall_s_timed": round(wall, 3),
+        "cpu_baseline": None,
+    }
+
+
+def run_prefill(args, torch):
+    """Prefill MoE layer: M=512 tokens, 256 FP4 experts, top-6 with Zipf(1.1)
+    popularity drawn without replacement per token, routed experts only (the
+    shared expert is timed separately as an extra); one hsmoe_moe_prefill call
+    (group, gate/up, down, combine) per step, steps captured in a HIP graph."""
+    from home_seek_amd import expert_store, ops, synthetic
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    m = 512
+    store = expert_store.HbmExpertStore(1, E, D, I, dev, with_shared=True)
+    store.fill_synthetic(args.seed)
+    x = synthetic.hidden(args.seed, 5000, m, D, dev)
+    idx_h, w_h = synthetic.zipf_routing(args.seed, m, E, K)
+    idx, w = torch.as_tensor(idx_h, device=dev), torch.as_tensor(w_h, device=dev)
+    counts = [int(c) for c in __import__("numpy").bincount(idx_h.reshape(-1), minlength=E)]
+    touched = sum(1 for c in counts if c)
+    table, shared = store.table(0), store.shared_entry(0)
+    out = torch.empty(m, D, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+
+    def timed(sh, steps, warmup):
+        fn = lambda: ops.moe_prefill(x, idx, w, table, ops.SCALE_E8M0, sh, 10.0, out_bf16=out, i=I)
+        stream = torch.cuda.Stream()
+        with torch.cuda.stream(stream):
+            fn()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                fn()
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    ms = timed(None, args.steps, args.warmup)
+    ms_sh = timed(shared, max(5, args.steps // 5), 2)
+    routed_bytes = touched * EXPERT_BYTES
+    io_bytes = m * D * 2 * 2 + m * K * 12
+    flops = 3 * 2 * D * I * m * K  # gate, up, down of every (token, expert) pair
+    gbs = routed_bytes / (ms * 1e-3) / 1e9
+    ach = (routed_bytes + io_bytes) / (ms * 1e-3) / 1e9
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {
+        "metric": "MoE layer FP4 expert GB/s (% HBM peak) at M=1/M=3; MTP-verify decode tok/s",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp4-e2m1 weights, bf16 MFMA, fp32 accumulate",
+        "data": "synthetic (seeded on device; Zipf(1.1) routing seeded on the host)",
+        "config": {
+            "workload": f"prefill MoE layer, M={m} tokens, D={D} I={I}, {E} FP4 experts top-{K}, Zipf(1.1) "
+                        "popularity (grouped gate/up + down GEMM), routed experts only",
+            "global_batch": m,
+            "seq_len": m,
+            "parallelism": "none (1 GPU)",
+        },
+        "touched_experts": touched,
+        "max_tokens_per_expert": max(counts),
+        "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "mfma_tflops": round(tflops, 2),
+        "pct_bf16_mfma_peak": round(100.0 * tflops / 2500.0, 3),
+        "with_shared_expert": {"ms": round(ms_sh, 5),
+                               "gbs": round((routed_bytes + SHARED_GATE_UP + SHARED_DOWN) / (ms_sh * 1e-3) / 1e9, 1)},
+        "roofline": {"bound": "hbm", "kernel": "hsmoe_moe_prefill call (group + gate/up + down + combine launches)",
+                     "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": routed_bytes + io_bytes, "avg_launch_us": round(ms * 1e3, 2)},
         "cpu_baseline": None,
     }
 

@@ -1,0 +1,482 @@
+// Routed-expert SwiGLU FFN for many tokens (prefill): a grouped GEMM over the
+// experts the tokens select, each expert's weights streamed from HBM once per
+// chunk of up to 32 of its tokens.
+//
+// Restates FusedMoEFFN._forward_legacy at B > 8 and the FP4 grouped route of
+// fused_expert_ffn_triton (fused_moe.py:269-380, 458-551) plus the shared
+// expert add of _forward_ffn (engine.py:1530-1536), with the arithmetic of
+// the decode kernels:
+//   gate = x W1^T, up = x W3^T (fp32 accumulation of exact bf16 products);
+//   a = w * min(g,L) sigmoid(min(g,L)) clamp(u,-L,L);  y = a W2^T
+//   out[t] = sum_j y[t, j] (slot order) + shared(t)
+// W = bf16(dequant(FP4)) decoded in registers; the activation enters the down
+// GEMM as a bf16 hi + lo pair.  Unlike the reference's dense union GEMM
+// (every token through every selected expert), only the (token, expert) pairs
+// that routing selects are computed.
+//
+// Four launches, no host synchronisation:
+//   group    one workgroup: pairs (t, j) bucketed by expert in (t, j) order
+//            (stable, deterministic), then the shared expert's M pairs; the
+//            bucket of each expert is cut into chunks of <= 32 pairs.
+//   gate_up  grid (chunk, 64-row block of I): wave w takes rows +16w..+16 of
+//            W1 and W3 over all of D; the chunk's 32 token rows of x are staged
+//            in LDS 512 columns at a time while the next 512 columns of weights
+//            are already in flight.  Writes the weighted activation (hi, lo).
+//   down     grid (chunk, 64-row block of D): same structure over W2 with the
+//            activation tile (hi and lo) staged 256 columns at a time; writes
+//            one fp32 partial row per pair (no atomics).
+//   combine  out[t] = partials of t's pairs in slot order, then the shared one.
+// The grids are sized for the most chunks the routing can produce; workgroups
+// past the actual count (read from the workspace) exit at once.
+#include <math.h>
+
+#include "hsmoe_common.h"
+#include "hsmoe_internal.h"
+#include "hsmoe_tiles.h"
+
+namespace hsmoe {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kChunk = 32;        // tokens per chunk (two 16-token MFMA tiles)
+constexpr int kRows = 64;         // weight rows per workgroup (16 per wave)
+constexpr int kGuCols = 512;      // x columns staged per K-chunk (4 steps)
+constexpr int kDnCols = 256;      // activation columns staged per K-chunk (2 steps)
+constexpr int kPad = 8;           // bf16 elements of padding per LDS row
+constexpr int kMaxPairs = 16384;  // m * top_k per call (LDS of the group kernel)
+constexpr int kMaxExperts = 1024;
+
+struct Header {
+  int n_routed_chunks;  // chunks of routed experts; the shared expert's follow
+  int n_pairs;
+};
+
+struct PrefillParams {
+  const uint16_t* x;       // bf16 [m, d]
+  const int64_t* idx;      // [m, top_k]
+  const float* wts;        // [m, top_k]
+  const uint64_t* table;   // [n_experts][6]
+  const uint64_t* shared;  // [6] or null
+  Header* hdr;
+  int* pair_tok;           // [max_pairs] token of pair p
+  float* pair_w;           // [max_pairs] routing weight of pair p
+  int* pidx;               // [m][top_k + 1] pair of (t, j); j = top_k: shared; -1 = none
+  int* chunk_e;            // [max_chunks] expert (n_experts = shared)
+  int* chunk_p0;           // [max_chunks] first pair
+  int* chunk_n;            // [max_chunks] pairs in the chunk
+  uint16_t* act_hi;        // bf16 [max_pairs][i]
+  uint16_t* act_lo;        // bf16 [max_pairs][i]
+  float* part;             // fp32 [max_pairs][d]
+  float* out_f32;          // [m, d] or null
+  uint16_t* out_bf16;      // [m, d] or null
+  int n_experts;
+  int m, d, i, top_k;
+  int scale_fmt;  // kFp4E8M0 or kFp4F32 for routed FP4 experts
+  float limit;
+};
+
+// ---------------------------------------------------------------- group
+__global__ void __launch_bounds__(kThreads) prefill_group_kernel(PrefillParams p) {
+  __shared__ int s_e[kMaxPairs];
+  __shared__ int s_cnt[kMaxExperts + 1];
+  __shared__ int s_off[kMaxExperts + 2];
+  __shared__ int s_choff[kMaxExperts + 2];
+  const int E = p.n_experts, K = p.top_k, P = p.m * K;
+  for (int q = threadIdx.x; q < P; q += kThreads) {
+    const int64_t e = p.idx[q];
+    const bool ok = e >= 0 && e < E && p.table[e * 6] != 0;
+    s_e[q] = ok ? (int)e : -1;
+    if (!ok) p.pidx[(q / K) * (K + 1) + q % K] = -1;
+  }
+  __syncthreads();
+  // counts: one thread per expert scans the pair list (broadcast LDS reads)
+  for (int e = threadIdx.x; e < E; e += kThreads) {
+    int c = 0;
+    for (int q = 0; q < P; ++q) c += s_e[q] == e;
+    s_cnt[e] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int off = 0, ch = 0;
+    for (int e = 0; e < E; ++e) {
+      s_off[e] = off;
+      s_choff[e] = ch;
+      off += s_cnt[e];
+      ch += (s_cnt[e] + kChunk - 1) / kChunk;
+    }
+    s_off[E] = off;  // the shared expert's pairs follow the routed ones
+    s_choff[E] = ch;
+    const int nsh = p.shared ? p.m : 0;
+    p.hdr->n_pairs = off + nsh;
+    p.hdr->n_routed_chunks = ch;
+  }
+  __syncthreads();
+  // pairs of expert e in (t, j) order, and its chunks
+  for (int e = threadIdx.x; e < E; e += kThreads) {
+    int pos = s_off[e];
+    if (s_cnt[e] > 0) {
+      for (int q = 0; q < P; ++q) {
+        if (s_e[q] != e) continue;
+        p.pair_tok[pos] = q / K;
+        p.pair_w[pos] = p.wts[q];
+        p.pidx[(q / K) * (K + 1) + q % K] = pos;
+        ++pos;
+      }
+    }
+    for (int c = 0, ch = s_choff[e]; c < s_cnt[e]; c += kChunk, ++ch) {
+      p.chunk_e[ch] = e;
+      p.chunk_p0[ch] = s_off[e] + c;
+      p.chunk_n[ch] = min(kChunk, s_cnt[e] - c);
+    }
+  }
+  for (int t = threadIdx.x; t < p.m; t += kThreads) {
+    const int pos = s_off[E] + t;
+    if (p.shared) {
+      p.pair_tok[pos] = t;
+      p.pair_w[pos] = 1.0f;
+    }
+    p.pidx[t * (K + 1) + K] = p.shared ? pos : -1;
+    if (p.shared && t % kChunk == 0) {
+      const int ch = s_choff[E] + t / kChunk;
+      p.chunk_e[ch] = E;
+      p.chunk_p0[ch] = pos;
+      p.chunk_n[ch] = min(kChunk, p.m - t);
+    }
+  }
+}
+
+// B operand (16 token columns x 32 k) from an LDS tile [kChunk][cols + kPad]:
+// lane (c, g) takes token tile*16 + c, columns 128*st + 32g + 8j .. +8.
+__device__ __forceinline__ bf16x8 tile_frag(const uint16_t* t, int cols, int tile, int c, int g, int st, int j) {
+  return *reinterpret_cast<const bf16x8*>(t + (tile * 16 + c) * (cols + kPad) + st * 128 + g * 32 + 8 * j);
+}
+
+// Copies columns [c0, c0 + cols) of rows src_row(tt) (tt < n; zeros above) into
+// an LDS tile [kChunk][cols + kPad], 16 bytes per thread per pass.
+template <typename RowPtr>
+__device__ __forceinline__ void stage_rows(uint16_t* t, int cols, int n, RowPtr src_row) {
+  const int per_row = cols / 8;
+  for (int u = threadIdx.x; u < kChunk * per_row; u += kThreads) {
+    const int tt = u / per_row, cc = u - tt * per_row;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (tt < n) v = *reinterpret_cast<const uint4*>(src_row(tt) + cc * 8);
+    *reinterpret_cast<uint4*>(t + tt * (cols + kPad) + cc * 8) = v;
+  }
+}
+
+struct Chunk {
+  int e, p0, n;
+  const uint64_t* ent;
+};
+
+// Chunk q of the routed experts (kShared = false) or of the shared expert.
+template <bool kShared>
+__device__ __forceinline__ bool load_chunk(const PrefillParams& p, int q, Chunk& ch) {
+  const int nr = p.hdr->n_routed_chunks;
+  if (kShared) {
+    if (q * kChunk >= p.m) return false;
+    q += nr;
+  } else if (q >= nr) {
+    return false;
+  }
+  ch.e = p.chunk_e[q];
+  ch.p0 = p.chunk_p0[q];
+  ch.n = p.chunk_n[q];
+  ch.ent = kShared ? p.shared : p.table + (int64_t)ch.e * 6;
+  return true;
+}
+
+// Software pipeline over weight batches of kB steps: the batch after the one
+// being multiplied is always in flight.  Step s of the stream is column block
+// 128 s .. 128 s + 127 of the weight rows; K-chunks of kSteps steps have their
+// token tile staged in LDS by stage(kc) (block-wide, between barriers) before
+// their batches are used.
+template <int F, int kB, int kSteps, int kMats, typename Stage, typename Mul>
+__device__ __forceinline__ void stream_rows(const uint64_t* ent, int w_slot, int64_t row, int64_t k, int g,
+                                            Stage&& stage, Mul&& mul) {
+  static_assert(kSteps % kB == 0, "batches must tile a K-chunk");
+  const int total = (int)(k / 128);
+  Batch<F, kB> n[kMats];
+#pragma unroll
+  for (int q = 0; q < kMats; ++q) n[q].load(ent[w_slot + 2 * q], ent[w_slot + 2 * q + 1], row, k, 0, g);
+  for (int kc = 0; kc * kSteps < total; ++kc) {
+    __syncthreads();
+    stage(kc);
+    __syncthreads();
+#pragma unroll
+    for (int sb = 0; sb < kSteps / kB; ++sb) {
+      Batch<F, kB> c[kMats];
+#pragma unroll
+      for (int q = 0; q < kMats; ++q) c[q] = n[q];
+      const int nxt = kc * kSteps + (sb + 1) * kB;
+      if (nxt < total) {
+#pragma unroll
+        for (int q = 0; q < kMats; ++q) n[q].load(ent[w_slot + 2 * q], ent[w_slot + 2 * q + 1], row, k, nxt, g);
+      }
+      mul(c, sb * kB);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- gate / up
+// Wave rows r0 .. r0+15 of W1 and W3 against the chunk's tokens; lane (r, g)
+// ends holding rows r0 + 4g + q of token tile*16 + r.
+template <int F, int kB>
+__device__ void gate_up_chunk(const PrefillParams& p, const Chunk& ch, int r0, uint16_t* xs, const int* s_tok) {
+  constexpr int kSteps = kGuCols / 128;
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int ntile = (ch.n + 15) / 16;
+  f32x4 ag[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}}, au[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+  stream_rows<F, kB, kSteps, 2>(
+      ch.ent, 0, r0 + r, p.d, g,
+      [&](int kc) {
+        stage_rows(xs, kGuCols, ch.n, [&](int tt) { return p.x + (int64_t)s_tok[tt] * p.d + kc * kGuCols; });
+      },
+      [&](const Batch<F, kB>* w, int s0) {
+#pragma unroll
+        for (int tile = 0; tile < 2; ++tile) {
+          if (tile >= ntile) break;
+#pragma unroll
+          for (int b = 0; b < kB; ++b) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const bf16x8 xf = tile_frag(xs, kGuCols, tile, r, g, s0 + b, j);
+              ag[tile] = mfma16x16x32(w[0].frag(b, j, g), xf, ag[tile]);
+              au[tile] = mfma16x16x32(w[1].frag(b, j, g), xf, au[tile]);
+            }
+          }
+        }
+      });
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile) {
+    const int tt = tile * 16 + r;
+    if (tile >= ntile || tt >= ch.n) continue;
+    const int64_t pr = ch.p0 + tt;
+    const float wt = p.pair_w[pr];
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float a = __fmul_rn(wt, swiglu(ag[tile][q], au[tile][q], p.limit));
+      hi[q] = f32_to_bf16_bits(a);
+      lo[q] = f32_to_bf16_bits(__fadd_rn(a, -bf16_bits_to_f32(hi[q])));
+    }
+    const int64_t o = pr * p.i + r0 + 4 * g;
+    *reinterpret_cast<uint2*>(p.act_hi + o) = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
+    *reinterpret_cast<uint2*>(p.act_lo + o) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
+  }
+}
+
+// F: format of the chunks' weights (routed FP4 of the call's scale kind, or
+// the shared expert's FP8); table entries without scales take the bf16 path.
+template <int F, bool kShared>
+__global__ void __launch_bounds__(kThreads) prefill_gate_up_kernel(PrefillParams p) {
+  __shared__ __align__(16) uint16_t xs[kChunk * (kGuCols + kPad)];
+  __shared__ int s_tok[kChunk];
+  const int nrb = p.i / kRows;
+  Chunk ch;
+  if (!load_chunk<kShared>(p, blockIdx.x / nrb, ch)) return;
+  if (threadIdx.x < kChunk) s_tok[threadIdx.x] = threadIdx.x < ch.n ? p.pair_tok[ch.p0 + threadIdx.x] : 0;
+  const int r0 = (blockIdx.x % nrb) * kRows + 16 * (threadIdx.x >> 6);
+  if (ch.ent[1]) gate_up_chunk<F, (F == kFp8Block ? 2 : 4)>(p, ch, r0, xs, s_tok);
+  else gate_up_chunk<kBf16, 1>(p, ch, r0, xs, s_tok);
+}
+
+// ---------------------------------------------------------------- down
+template <int F, int kB>
+__device__ void down_chunk(const PrefillParams& p, const Chunk& ch, int r0, uint16_t* hs, uint16_t* ls) {
+  constexpr int kSteps = kDnCols / 128;
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int ntile = (ch.n + 15) / 16;
+  f32x4 acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+  stream_rows<F, kB, kSteps, 1>(
+      ch.ent, 4, r0 + r, p.i, g,
+      [&](int kc) {
+        stage_rows(hs, kDnCols, ch.n, [&](int tt) { return p.act_hi + (int64_t)(ch.p0 + tt) * p.i + kc * kDnCols; });
+        stage_rows(ls, kDnCols, ch.n, [&](int tt) { return p.act_lo + (int64_t)(ch.p0 + tt) * p.i + kc * kDnCols; });
+      },
+      [&](const Batch<F, kB>* w, int s0) {
+#pragma unroll
+        for (int tile = 0; tile < 2; ++tile) {
+          if (tile >= ntile) break;
+#pragma unroll
+          for (int b = 0; b < kB; ++b) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const bf16x8 wf = w[0].frag(b, j, g);
+              acc[tile] = mfma16x16x32(wf, tile_frag(hs, kDnCols, tile, r, g, s0 + b, j), acc[tile]);
+              acc[tile] = mfma16x16x32(wf, tile_frag(ls, kDnCols, tile, r, g, s0 + b, j), acc[tile]);
+            }
+          }
+        }
+      });
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile) {
+    const int tt = tile * 16 + r;
+    if (tile >= ntile || tt >= ch.n) continue;
+    float* o = p.part + (int64_t)(ch.p0 + tt) * p.d + r0 + 4 * g;
+    *reinterpret_cast<float4*>(o) = make_float4(acc[tile][0], acc[tile][1], acc[tile][2], acc[tile][3]);
+  }
+}
+
+template <int F, bool kShared>
+__global__ void __launch_bounds__(kThreads) prefill_down_kernel(PrefillParams p) {
+  __shared__ __align__(16) uint16_t hs[kChunk * (kDnCols + kPad)];
+  __shared__ __align__(16) uint16_t ls[kChunk * (kDnCols + kPad)];
+  const int nrb = p.d / kRows;
+  Chunk ch;
+  if (!load_chunk<kShared>(p, blockIdx.x / nrb, ch)) return;
+  const int r0 = (blockIdx.x % nrb) * kRows + 16 * (threadIdx.x >> 6);
+  if (ch.ent[1]) down_chunk<F, 2>(p, ch, r0, hs, ls);
+  else down_chunk<kBf16, 1>(p, ch, r0, hs, ls);
+}
+
+// ---------------------------------------------------------------- combine
+// grid (m, d / 1024): thread -> 4 consecutive columns of one token.
+__global__ void __launch_bounds__(kThreads) prefill_combine_kernel(PrefillParams p) {
+  const int t = blockIdx.x;
+  const int col = (blockIdx.y * kThreads + threadIdx.x) * 4;
+  if (col >= p.d) return;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int* pi = p.pidx + (int64_t)t * (p.top_k + 1);
+  for (int j = 0; j <= p.top_k; ++j) {
+    const int pr = pi[j];
+    if (pr < 0) continue;
+    const float4 v = *reinterpret_cast<const float4*>(p.part + (int64_t)pr * p.d + col);
+    acc.x = __fadd_rn(acc.x, v.x);
+    acc.y = __fadd_rn(acc.y, v.y);
+    acc.z = __fadd_rn(acc.z, v.z);
+    acc.w = __fadd_rn(acc.w, v.w);
+  }
+  const int64_t o = (int64_t)t * p.d + col;
+  if (p.out_f32) *reinterpret_cast<float4*>(p.out_f32 + o) = acc;
+  if (p.out_bf16)
+    *reinterpret_cast<uint2*>(p.out_bf16 + o) =
+        make_uint2(f32_to_bf16_bits(acc.x) | (f32_to_bf16_bits(acc.y) << 16),
+                   f32_to_bf16_bits(acc.z) | (f32_to_bf16_bits(acc.w) << 16));
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+struct Layout {
+  size_t hdr, pair_tok, pair_w, pidx, chunk_e, chunk_p0, chunk_n, act_hi, act_lo, part, total;
+};
+
+int64_t max_pairs(int64_t m, int top_k) { return m * top_k + m; }
+// Chunks of the routed experts: sum over experts of ceil(n_e / kChunk) <=
+// (experts with a pair) + (pairs) / kChunk.
+int64_t max_routed_chunks(int64_t m, int64_t n_experts, int top_k) {
+  const int64_t pk = m * top_k;
+  return (n_experts < pk ? n_experts : pk) + (pk + kChunk - 1) / kChunk;
+}
+int64_t max_chunks(int64_t m, int64_t n_experts, int top_k) {
+  return max_routed_chunks(m, n_experts, top_k) + (m + kChunk - 1) / kChunk;
+}
+
+Layout layout(int64_t m, int64_t d, int64_t i, int64_t n_experts, int top_k) {
+  const int64_t P = max_pairs(m, top_k), C = max_chunks(m, n_experts, top_k);
+  Layout L;
+  size_t o = 0;
+  L.hdr = o;
+  o += 256;
+  L.pair_tok = o;
+  o += align256((size_t)P * 4);
+  L.pair_w = o;
+  o += align256((size_t)P * 4);
+  L.pidx = o;
+  o += align256((size_t)m * (top_k + 1) * 4);
+  L.chunk_e = o;
+  o += align256((size_t)C * 4);
+  L.chunk_p0 = o;
+  o += align256((size_t)C * 4);
+  L.chunk_n = o;
+  o += align256((size_t)C * 4);
+  L.act_hi = o;
+  o += align256((size_t)P * i * 2);
+  L.act_lo = o;
+  o += align256((size_t)P * i * 2);
+  L.part = o;
+  o += align256((size_t)P * d * 4);
+  L.total = o;
+  return L;
+}
+
+}  // namespace
+}  // namespace hsmoe
+
+using namespace hsmoe;
+
+extern "C" size_t hsmoe_moe_prefill_workspace_size(int64_t m, int64_t d, int64_t i, int64_t n_experts, int top_k) {
+  if (m < 1 || d < 1 || i < 1 || n_experts < 1 || top_k < 1) return 0;
+  return layout(m, d, i, n_experts, top_k).total;
+}
+
+extern "C" int hsmoe_moe_prefill(const void* x, int64_t m, int64_t d, int64_t i, const int64_t* topk_idx,
+                                 const float* topk_w, int top_k, const uint64_t* expert_table, int64_t n_experts,
+                                 int scale_kind, const uint64_t* shared, float swiglu_limit, float* out_f32,
+                                 void* out_bf16, void* workspace, size_t workspace_bytes, hsmoe_stream_t stream) {
+  const char* name = "hsmoe_moe_prefill";
+  if (!x || !topk_idx || !topk_w || !expert_table || (!out_f32 && !out_bf16))
+    return fail(HSMOE_ERR_ARG, "%s: null pointer or no output", name);
+  if (scale_kind != HSMOE_SCALE_E8M0 && scale_kind != HSMOE_SCALE_F32)
+    return fail(HSMOE_ERR_ARG, "%s: unknown scale_kind %d", name, scale_kind);
+  if (n_experts < 1 || n_experts > kMaxExperts || top_k < 1 || top_k > 16 || m < 1 || m * top_k > kMaxPairs)
+    return fail(HSMOE_ERR_SHAPE, "%s: need 1 <= n_experts <= %d, 1 <= top_k <= 16, 1 <= m*top_k <= %d", name,
+                kMaxExperts, kMaxPairs);
+  if (d % 1024 != 0 || i % 512 != 0 || d > 65536 || i > 65536)
+    return fail(HSMOE_ERR_SHAPE, "%s: d must be a multiple of 1024 and i of 512 (d=%lld i=%lld)", name, (long long)d,
+                (long long)i);
+  if (!aligned(x, 16) || (out_f32 && !aligned(out_f32, 16)) || (out_bf16 && !aligned(out_bf16, 8)))
+    return fail(HSMOE_ERR_SHAPE, "%s: x and out_f32 must be 16-byte aligned, out_bf16 8-byte aligned", name);
+  const Layout L = layout(m, d, i, n_experts, top_k);
+  if (!workspace || workspace_bytes < L.total || !aligned(workspace, 256))
+    return fail(HSMOE_ERR_WORKSPACE, "%s: workspace of %zu bytes (256-byte aligned) needed", name, L.total);
+  char* ws = (char*)workspace;
+  PrefillParams p;
+  p.x = (const uint16_t*)x;
+  p.idx = topk_idx;
+  p.wts = topk_w;
+  p.table = expert_table;
+  p.shared = shared;
+  p.hdr = (Header*)(ws + L.hdr);
+  p.pair_tok = (int*)(ws + L.pair_tok);
+  p.pair_w = (float*)(ws + L.pair_w);
+  p.pidx = (int*)(ws + L.pidx);
+  p.chunk_e = (int*)(ws + L.chunk_e);
+  p.chunk_p0 = (int*)(ws + L.chunk_p0);
+  p.chunk_n = (int*)(ws + L.chunk_n);
+  p.act_hi = (uint16_t*)(ws + L.act_hi);
+  p.act_lo = (uint16_t*)(ws + L.act_lo);
+  p.part = (float*)(ws + L.part);
+  p.out_f32 = out_f32;
+  p.out_bf16 = (uint16_t*)out_bf16;
+  p.n_experts = (int)n_experts;
+  p.m = (int)m;
+  p.d = (int)d;
+  p.i = (int)i;
+  p.top_k = top_k;
+  p.scale_fmt = scale_kind == HSMOE_SCALE_E8M0 ? kFp4E8M0 : kFp4F32;
+  p.limit = swiglu_limit;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t C = max_routed_chunks(m, n_experts, top_k), CS = shared ? (m + kChunk - 1) / kChunk : 0;
+  hipLaunchKernelGGL(prefill_group_kernel, dim3(1), dim3(kThreads), 0, st, p);
+  int rc = check_launch(name);
+  if (rc) return rc;
+  const dim3 blk(kThreads), gu((unsigned)(C * (i / kRows))), dn((unsigned)(C * (d / kRows)));
+  if (scale_kind == HSMOE_SCALE_E8M0) hipLaunchKernelGGL((prefill_gate_up_kernel<kFp4E8M0, false>), gu, blk, 0, st, p);
+  else hipLaunchKernelGGL((prefill_gate_up_kernel<kFp4F32, false>), gu, blk, 0, st, p);
+  if ((rc = check_launch(name))) return rc;
+  if (CS) {
+    hipLaunchKernelGGL((prefill_gate_up_kernel<kFp8Block, true>), dim3((unsigned)(CS * (i / kRows))), blk, 0, st, p);
+    if ((rc = check_launch(name))) return rc;
+  }
+  if (scale_kind == HSMOE_SCALE_E8M0) hipLaunchKernelGGL((prefill_down_kernel<kFp4E8M0, false>), dn, blk, 0, st, p);
+  else hipLaunchKernelGGL((prefill_down_kernel<kFp4F32, false>), dn, blk, 0, st, p);
+  if ((rc = check_launch(name))) return rc;
+  if (CS) {
+    hipLaunchKernelGGL((prefill_down_kernel<kFp8Block, true>), dim3((unsigned)(CS * (d / kRows))), blk, 0, st, p);
+    if ((rc = check_launch(name))) return rc;
+  }
+  hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)m, (unsigned)(d / (4 * kThreads))), dim3(kThreads), 0,
+                     st, p);
+  return check_launch(name);
+}

@@ -55,9 +55,13 @@ def _bf16_entry(w: tuple, dev: torch.device):
 def _run_decode_chunks(x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor, table: torch.Tensor,
                        scale_kind: int, shared: Optional[torch.Tensor], limit: float, d: int, i: int,
                        out_f32: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Runs the M <= 8 kernel over token chunks of 8."""
+    """M <= 8: the decode kernel; more tokens: the prefill grouped GEMM (or, for
+    hidden sizes it does not tile, the decode kernel over chunks of 8 tokens)."""
     m = x.shape[0]
     out = torch.empty(m, d, dtype=torch.bfloat16, device=x.device)
+    if m > ops.MAX_DECODE_TOKENS and d % 1024 == 0:
+        ops.moe_prefill(x, topk_idx, topk_w, table, scale_kind, shared, limit, out_bf16=out, out_f32=out_f32, i=i)
+        return out
     step = ops.MAX_DECODE_TOKENS
     for a in range(0, m, step):
         b = min(m, a + step)

@@ -169,6 +169,40 @@ def moe_decode(x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor, ta
     return out_bf16, out_f32
 
 
+MAX_PREFILL_PAIRS = 16384  # m * top_k per hsmoe_moe_prefill call
+
+
+def moe_prefill(x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor, table: torch.Tensor,
+                scale_kind: int, shared: torch.Tensor | None = None, swiglu_limit: float = 10.0,
+                out_bf16: torch.Tensor | None = None, out_f32: torch.Tensor | None = None, i: int | None = None):
+    """Routed (+ shared) SwiGLU FFN for any number of tokens as a grouped GEMM
+    (hsmoe_moe_prefill); returns (out_bf16, out_f32).  Token blocks of at most
+    MAX_PREFILL_PAIRS // top_k rows go to one call each."""
+    dev = require_cuda(x, topk_idx, topk_w, table, shared)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"hidden states must be bf16, got {x.dtype}")
+    if i is None:
+        raise ValueError("intermediate size i is required")
+    x = x.contiguous()
+    m, d = x.shape
+    topk_idx = topk_idx.to(torch.int64).reshape(m, -1).contiguous()
+    topk_w = topk_w.to(torch.float32).reshape(m, -1).contiguous()
+    k = topk_idx.shape[1]
+    if out_bf16 is None:
+        out_bf16 = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
+    step = max(1, MAX_PREFILL_PAIRS // k)
+    for a in range(0, m, step):
+        b = min(m, a + step)
+        nbytes = lib().hsmoe_moe_prefill_workspace_size(b - a, d, i, table.shape[0], k)
+        ws = _workspace(dev, "prefill", nbytes)
+        rc = lib().hsmoe_moe_prefill(ptr(x[a:b]), b - a, d, i, ptr(topk_idx[a:b]), ptr(topk_w[a:b]), k, ptr(table),
+                                     table.shape[0], scale_kind, ptr(shared), swiglu_limit,
+                                     None if out_f32 is None else ptr(out_f32[a:b]), ptr(out_bf16[a:b]), ptr(ws),
+                                     ws.numel(), stream_ptr(dev))
+        check(rc, "hsmoe_moe_prefill")
+    return out_bf16, out_f32
+
+
 def moe_decode_stage(stage: int, x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor,
                      table: torch.Tensor, scale_kind: int, shared: torch.Tensor | None, swiglu_limit: float,
                      d: int, i: int, out_bf16: torch.Tensor | None = None, out_f32: torch.Tensor | None = None):

@@ -93,3 +93,21 @@ def router_weights(seed: int, layer: int, n_experts: int, d: int, device):
 
 def hidden(seed: int, case: int, m: int, d: int, device) -> torch.Tensor:
     return normal_bf16(seed, tag(KIND_HIDDEN, 0, case), (m, d), 0.0, 1.0, device)
+
+
+def zipf_routing(seed: int, m: int, n_experts: int, top_k: int = 6, s: float = 1.1, scaling: float = 1.5):
+    """Prefill routing with Zipf(s)-skewed expert popularity, drawn without
+    replacement per token (Gumbel-top-k over log p_e), on the host (numpy PCG64):
+    expert of popularity rank r has p ~ 1/(r+1)^s, ranks assigned to ids by a
+    seeded permutation; weights are the chosen p renormalised to `scaling`.
+    -> (idx int64 [m, top_k], w fp32 [m, top_k]) numpy arrays."""
+    import numpy as np
+
+    rng = np.random.Generator(np.random.PCG64(seed))
+    logp = -s * np.log(np.arange(1, n_experts + 1, dtype=np.float64))
+    logp = logp[np.argsort(rng.permutation(n_experts))]  # id -> popularity
+    g = logp[None, :] + rng.gumbel(size=(m, n_experts))
+    idx = np.argsort(-g, axis=1, kind="stable")[:, :top_k].astype(np.int64)
+    p = np.exp(logp[idx])
+    w = (p / p.sum(axis=1, keepdims=True) * scaling).astype(np.float32)
+    return idx, w

@@ -164,6 +164,29 @@ int hsmoe_moe_layer_decode(const void* x_dev, int64_t m, int64_t d, int64_t i, c
 size_t hsmoe_moe_layer_status_offset(void);
 
 /* ---------------------------------------------------------------------------
+ * Routed-expert SwiGLU FFN for many tokens (prefill, m > 8): a grouped GEMM
+ * over the (token, expert) pairs the routing selects.  Replaces
+ * FusedMoEFFN.forward at B > 8 (reference src/home_seek/fused_moe.py:447-551,
+ * _forward_legacy, whose union route runs every token through every selected
+ * expert) and the FP4 grouped route of fused_expert_ffn_triton
+ * (fused_moe.py:269-380), plus the shared-expert add of _forward_ffn
+ * (src/home_seek/inference_engine/engine.py:1530-1536).
+ * Arguments, formats and results as hsmoe_moe_decode (same arithmetic:
+ * exact bf16 products, fp32 accumulation, fp32 SwiGLU, hi/lo activation),
+ * with out[t] = sum_j topk_w[t, j] * FFN_{topk_idx[t, j]}(x[t]) in slot order j,
+ * then + shared FFN(x[t]); a (t, j) with an invalid id or absent expert adds
+ * nothing.  Each selected expert's weights are read once per chunk of up to
+ * 32 of its tokens.  Deterministic (no atomics).
+ * 1 <= m * top_k <= 16384, n_experts <= 1024, top_k <= 16, d % 1024 == 0,
+ * i % 512 == 0; x and out_f32 16-byte aligned, out_bf16 8-byte aligned.
+ * The workspace (any contents) must hold hsmoe_moe_prefill_workspace_size bytes. */
+size_t hsmoe_moe_prefill_workspace_size(int64_t m, int64_t d, int64_t i, int64_t n_experts, int top_k);
+int hsmoe_moe_prefill(const void* x_dev, int64_t m, int64_t d, int64_t i, const int64_t* topk_idx_dev,
+                      const float* topk_w_dev, int top_k, const uint64_t* expert_table_dev, int64_t n_experts,
+                      int scale_kind, const uint64_t* shared_dev, float swiglu_limit, float* out_f32_dev,
+                      void* out_bf16_dev, void* workspace_dev, size_t workspace_bytes, hsmoe_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * lm_head logits + greedy argmax + longest-prefix draft acceptance.
  * Replaces the logits / acceptance loop of _mtp_verify_batched
  * (reference src/home_seek/inference_engine/engine.py:2480-2497) and the greedy

@@ -1,0 +1,176 @@
+"""GPU parity of the prefill grouped GEMM (hsmoe_moe_prefill, m > 8 tokens)
+against the fp32 CPU oracle.
+
+Bars (the task's FFN bar, on fp32 outputs): rel-L2 <= 1e-3 and max-abs <= 2e-2
+against oracle.moe_layer_fp32; bf16 outputs within one bf16 rounding step of
+bf16(oracle) plus 2e-2.  At the full shape (M=512, 256 experts, Zipf(1.1)
+routing) the oracle checks a sample of tokens (outputs are per token), and the
+whole output is checked against the decode kernels run 8 tokens at a time
+(same bar) and for determinism.
+"""
+import numpy as np
+import pytest
+import torch
+
+from home_seek_amd import expert_store, fused_moe, ops, synthetic
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+SEED, K = 777, 6
+
+
+def check_close(got_f32, got_bf16, ref, what):
+    err = got_f32.astype(np.float64) - ref.astype(np.float64)
+    rel = np.linalg.norm(err) / np.linalg.norm(ref)
+    mx = np.abs(err).max()
+    print(f"[{what}] rel-L2 {rel:.3e} max-abs {mx:.3e}")
+    assert rel <= 1e-3 and mx <= 2e-2, (what, rel, mx)
+    gb, rb = orc.bf16_to_f32(got_bf16), orc.bf16_to_f32(orc.f32_to_bf16(ref))
+    assert not (np.abs(gb - rb) > np.abs(rb) * 2.0 ** -7 + 2e-2).any(), what
+
+
+class Model:
+    def __init__(self, dev, n_experts, d, i, layer=0):
+        self.E, self.d, self.i = n_experts, d, i
+        self.store = expert_store.HbmExpertStore(1, n_experts, d, i, dev, with_shared=True)
+        self.store.fill_synthetic(SEED, [0])
+        self._cache = {}
+
+    def expert(self, e):
+        if e not in self._cache:
+            self._cache[e] = orc.gen_fp4_expert(SEED, 0, e, self.d, self.i)
+        return self._cache[e]
+
+    def shared(self):
+        if "s" not in self._cache:
+            self._cache["s"] = orc.gen_shared_expert(SEED, 0, self.d, self.i)
+        return self._cache["s"]
+
+    def oracle(self, x, idx, w, shared=True):
+        ids = {int(e) for e in idx.reshape(-1) if 0 <= int(e) < self.E}
+        experts = {e: self.expert(e) for e in ids}
+        return orc.moe_layer_fp32(orc.to_np_bf16(x), idx, w, experts, self.shared() if shared else None, 10.0)
+
+
+@pytest.fixture(scope="module")
+def small(dev):
+    m = Model(dev, 32, 1024, 512)
+    torch.cuda.synchronize()
+    return m
+
+
+def run(model, x, idx, w, shared=True, table=None):
+    dev = x.device
+    f32 = torch.empty(x.shape[0], model.d, dtype=torch.float32, device=dev)
+    out, _ = ops.moe_prefill(x, torch.as_tensor(idx, device=dev), torch.as_tensor(w, device=dev),
+                             model.store.table(0) if table is None else table, ops.SCALE_E8M0,
+                             model.store.shared_entry(0) if shared else None, 10.0, out_f32=f32, i=model.i)
+    return out, f32
+
+
+@pytest.mark.parametrize("m", [9, 40, 100])
+def test_small_zipf_routing_matches_oracle(small, dev, m):
+    x = synthetic.hidden(SEED, m, m, small.d, dev)
+    idx, w = synthetic.zipf_routing(SEED + m, m, small.E, K)
+    out, f32 = run(small, x, idx, w)
+    ref = small.oracle(x, idx, w)
+    check_close(f32.cpu().numpy(), orc.to_np_bf16(out), ref, f"prefill m={m}")
+
+
+def test_hot_expert_spans_many_chunks(small, dev):
+    """One expert chosen by all 100 tokens (4 chunks of <= 32), in varying slots."""
+    m = 100
+    x = synthetic.hidden(SEED, 3, m, small.d, dev)
+    idx, w = synthetic.zipf_routing(SEED, m, small.E, K)
+    for t in range(m):
+        j = t % K
+        row = [e for e in idx[t] if e != 7][:K - 1]
+        row.insert(j, 7)
+        idx[t] = row
+    out, f32 = run(small, x, idx, w, shared=False)
+    ref = small.oracle(x, idx, w, shared=False)
+    check_close(f32.cpu().numpy(), orc.to_np_bf16(out), ref, "hot expert")
+
+
+def test_invalid_ids_absent_experts_and_empty_tokens(small, dev):
+    m = 20
+    x = synthetic.hidden(SEED, 4, m, small.d, dev)
+    idx, w = synthetic.zipf_routing(SEED + 4, m, small.E, K)
+    idx[0, 1] = -1
+    idx[1, 0] = small.E + 5
+    idx[2, :] = -1  # no routed expert: the shared expert alone
+    idx[3, :] = -1
+    table = small.store.table(0).clone()
+    table[idx[5, 2]] = 0  # absent expert (loader returned None)
+    absent = int(idx[5, 2])
+    out, f32 = run(small, x, idx, w, table=table)
+    ridx = idx.copy()
+    ridx[ridx == absent] = -1
+    ref = small.oracle(x, ridx, w)
+    check_close(f32.cpu().numpy(), orc.to_np_bf16(out), ref, "edge ids")
+    # no routed and no shared expert -> zeros
+    idx2 = np.full((12, K), -1, dtype=np.int64)
+    out2, f2 = run(small, x[:12], idx2, w[:12], shared=False)
+    assert torch.count_nonzero(f2) == 0 and torch.count_nonzero(out2) == 0
+
+
+def test_matches_decode_kernels_and_is_deterministic(small, dev):
+    m = 64
+    x = synthetic.hidden(SEED, 5, m, small.d, dev)
+    idx, w = synthetic.zipf_routing(SEED + 5, m, small.E, K)
+    out, f32 = run(small, x, idx, w)
+    out2, f2 = run(small, x, idx, w)
+    assert torch.equal(out, out2) and torch.equal(f32, f2)
+    dec = torch.empty_like(f32)
+    ti, tw = torch.as_tensor(idx, device=dev), torch.as_tensor(w, device=dev)
+    for a in range(0, m, 8):
+        ops.moe_decode(x[a:a + 8], ti[a:a + 8], tw[a:a + 8], small.store.table(0), ops.SCALE_E8M0,
+                       small.store.shared_entry(0), 10.0, out_f32=dec[a:a + 8], d=small.d, i=small.i)
+    check_close(f32.cpu().numpy(), orc.to_np_bf16(out), dec.cpu().numpy(), "prefill vs decode kernels")
+
+
+def test_fused_moe_forward_with_fp32_scales_and_bf16_experts(small, dev):
+    """FusedMoEFFN.forward at B > 8 with the reference's loader shapes: fp32
+    scales, 3-tuple bf16 weights and None."""
+    m = 24
+    moe = fused_moe.FusedMoEFFN(small.E, small.i, small.d, 10.0)
+    x = synthetic.hidden(SEED, 6, m, small.d, dev)
+    idx, w = synthetic.zipf_routing(SEED + 6, m, small.E, K)
+    ids = sorted({int(e) for e in idx.reshape(-1)})
+    absent, as_bf16 = ids[0], set(ids[1:4])
+
+    def loader(layer_idx, eid):
+        if eid == absent:
+            return None
+        w1, s1, w3, s3, w2, s2 = small.store.expert_views(0, eid)
+        if eid in as_bf16:
+            return ops.fp4_dequant_bf16(w1, s1), ops.fp4_dequant_bf16(w3, s3), ops.fp4_dequant_bf16(w2, s2)
+        return w1, s1.to(torch.float32), w3, s3.to(torch.float32), w2, s2.to(torch.float32)
+
+    out = moe.forward(x, torch.as_tensor(idx, device=dev), torch.as_tensor(w, device=dev), loader, 0)
+    ridx = idx.copy()
+    ridx[ridx == absent] = -1
+    ref = small.oracle(x, ridx, w, shared=False)
+    gb, rb = orc.bf16_to_f32(orc.to_np_bf16(out)), orc.bf16_to_f32(orc.f32_to_bf16(ref))
+    assert not (np.abs(gb - rb) > np.abs(rb) * 2.0 ** -7 + 2e-2).any()
+
+
+def test_full_shape_m512_zipf(dev):
+    """Config shape: M=512, D=4096, I=2048, 256 experts, Zipf(1.1) top-6 + shared."""
+    model = Model(dev, 256, 4096, 2048)
+    m = 512
+    x = synthetic.hidden(SEED, 512, m, model.d, dev)
+    idx, w = synthetic.zipf_routing(1234, m, model.E, K)
+    counts = np.bincount(idx.reshape(-1), minlength=model.E)
+    print(f"touched experts {np.count_nonzero(counts)}, max tokens/expert {counts.max()}")
+    out, f32 = run(model, x, idx, w)
+    sample = [0, 1, 2, 255, 256, 400, 510, 511]
+    ref = model.oracle(x[sample], idx[sample], w[sample])
+    check_close(f32[sample].cpu().numpy(), orc.to_np_bf16(out[sample]), ref, "M=512 sample")
+    dec = torch.empty_like(f32)
+    ti, tw = torch.as_tensor(idx, device=dev), torch.as_tensor(w, device=dev)
+    for a in range(0, m, 8):
+        ops.moe_decode(x[a:a + 8], ti[a:a + 8], tw[a:a + 8], model.store.table(0), ops.SCALE_E8M0,
+                       model.store.shared_entry(0), 10.0, out_f32=dec[a:a + 8], d=model.d, i=model.i)
+    check_close(f32.cpu().numpy(), orc.to_np_bf16(out), dec.cpu().numpy(), "M=512 vs decode kernels")
