@@ -23,6 +23,24 @@ enum ScaleKind : int {
   kScaleF32 = 1,   // one fp32 value per 32 columns
 };
 
+// ------------------------------------------------------------------ loads
+// A load through the global address space (global_load_*).  A pointer whose
+// address space the compiler cannot see (an address read from a table or a
+// parameter block) gives a flat load, which counts against lgkmcnt as well as
+// vmcnt: every wait for an LDS access would then also wait for it.
+template <typename T>
+__device__ __forceinline__ T ldg(const void* p) {
+  return *(const T __attribute__((address_space(1)))*)p;
+}
+// uint4 is a class (its copy would go through a generic reference): load the
+// native 4 x u32 vector instead.
+template <>
+__device__ __forceinline__ uint4 ldg<uint4>(const void* p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = *(const u32x4 __attribute__((address_space(1)))*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // ------------------------------------------------------------------ bits
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 

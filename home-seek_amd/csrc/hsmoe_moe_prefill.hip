@@ -14,17 +14,20 @@
 // (every token through every selected expert), only the (token, expert) pairs
 // that routing selects are computed.
 //
-// Four launches, no host synchronisation:
-//   group    one workgroup: pairs (t, j) bucketed by expert in (t, j) order
-//            (stable, deterministic), then the shared expert's M pairs; the
-//            bucket of each expert is cut into chunks of <= 32 pairs.
-//   gate_up  grid (chunk, 64-row block of I): wave w takes rows +16w..+16 of
-//            W1 and W3 over all of D; the chunk's 32 token rows of x are staged
-//            in LDS 512 columns at a time while the next 512 columns of weights
-//            are already in flight.  Writes the weighted activation (hi, lo).
-//   down     grid (chunk, 64-row block of D): same structure over W2 with the
-//            activation tile (hi and lo) staged 256 columns at a time; writes
-//            one fp32 partial row per pair (no atomics).
+// Launches (no host synchronisation):
+//   group    workgroup e buckets the pairs (t, j) routed to expert e, in (t, j)
+//            order (stable, deterministic); one more workgroup places the
+//            shared expert's M pairs.  Each bucket is cut into chunks of <= 32
+//            pairs.
+//   gate_up  grid (chunk, 64-row block of I), one launch for the routed
+//            experts and one for the shared expert: wave w takes rows
+//            +16w..+16 of W1 and W3 over all of D in K-chunks of 256 columns.
+//            While chunk kc is multiplied, the token tile of kc+1 is in flight
+//            to registers (then LDS) and the weights of kc+2 to a third
+//            register buffer.  Writes the weighted activation (hi, lo).
+//   down     grid (chunk, 128-row block of D), same pipeline over W2 (32 rows
+//            per wave) with the activation tile (hi and lo planes); writes one
+//            fp32 partial row per pair (no atomics).
 //   combine  out[t] = partials of t's pairs in slot order, then the shared one.
 // The grids are sized for the most chunks the routing can produce; workgroups
 // past the actual count (read from the workspace) exit at once.
@@ -39,11 +42,13 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kChunk = 32;        // tokens per chunk (two 16-token MFMA tiles)
-constexpr int kRows = 64;         // weight rows per workgroup (16 per wave)
-constexpr int kGuCols = 512;      // x columns staged per K-chunk (4 steps)
-constexpr int kDnCols = 256;      // activation columns staged per K-chunk (2 steps)
+constexpr int kGuRT = 1;          // 16-row tiles per wave, gate/up (W1 and W3)
+constexpr int kDnRT = 2;          // 16-row tiles per wave, down (W2)
+constexpr int kGuRows = 64 * kGuRT;  // weight rows per workgroup
+constexpr int kDnRows = 64 * kDnRT;
+constexpr int kCols = 256;        // columns per K-chunk (2 steps of 128)
 constexpr int kPad = 8;           // bf16 elements of padding per LDS row
-constexpr int kMaxPairs = 16384;  // m * top_k per call (LDS of the group kernel)
+constexpr int kMaxPairs = 12288;  // m * top_k per call (LDS of the group kernel)
 constexpr int kMaxExperts = 1024;
 
 struct Header {
@@ -76,72 +81,105 @@ struct PrefillParams {
 };
 
 // ---------------------------------------------------------------- group
+// Sum over the block of v (every thread passes its own value).
+__device__ __forceinline__ int block_sum(int v, int* s_red) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int t = 0;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) t += s_red[w];
+  return t;
+}
+
+// Workgroup e < n_experts places the pairs of expert e; workgroup n_experts
+// writes the header, the shared expert's pairs and the slots of invalid ids.
+// Every workgroup histograms the whole pair list in LDS, so the offsets of
+// expert e (pairs and chunks of the experts before it) need no second pass.
+// Within an expert, pairs keep (t, j) order: blocks of 256 pairs in order,
+// ranked by wave ballots.
 __global__ void __launch_bounds__(kThreads) prefill_group_kernel(PrefillParams p) {
   __shared__ int s_e[kMaxPairs];
-  __shared__ int s_cnt[kMaxExperts + 1];
-  __shared__ int s_off[kMaxExperts + 2];
-  __shared__ int s_choff[kMaxExperts + 2];
-  const int E = p.n_experts, K = p.top_k, P = p.m * K;
+  __shared__ int s_cnt[kMaxExperts];
+  __shared__ int s_red[kThreads / 64];
+  __shared__ int s_wc[kThreads / 64];
+  const int E = p.n_experts, K = p.top_k, P = p.m * K, me = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int e = threadIdx.x; e < E; e += kThreads) s_cnt[e] = 0;
+  __syncthreads();
   for (int q = threadIdx.x; q < P; q += kThreads) {
     const int64_t e = p.idx[q];
     const bool ok = e >= 0 && e < E && p.table[e * 6] != 0;
     s_e[q] = ok ? (int)e : -1;
-    if (!ok) p.pidx[(q / K) * (K + 1) + q % K] = -1;
+    if (ok) atomicAdd(&s_cnt[e], 1);
   }
   __syncthreads();
-  // counts: one thread per expert scans the pair list (broadcast LDS reads)
-  for (int e = threadIdx.x; e < E; e += kThreads) {
-    int c = 0;
-    for (int q = 0; q < P; ++q) c += s_e[q] == e;
-    s_cnt[e] = c;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int off = 0, ch = 0;
-    for (int e = 0; e < E; ++e) {
-      s_off[e] = off;
-      s_choff[e] = ch;
-      off += s_cnt[e];
-      ch += (s_cnt[e] + kChunk - 1) / kChunk;
+  if (me == E) {
+    int pairs = 0, chunks = 0;
+    for (int e = threadIdx.x; e < E; e += kThreads) {
+      pairs += s_cnt[e];
+      chunks += (s_cnt[e] + kChunk - 1) / kChunk;
     }
-    s_off[E] = off;  // the shared expert's pairs follow the routed ones
-    s_choff[E] = ch;
-    const int nsh = p.shared ? p.m : 0;
-    p.hdr->n_pairs = off + nsh;
-    p.hdr->n_routed_chunks = ch;
-  }
-  __syncthreads();
-  // pairs of expert e in (t, j) order, and its chunks
-  for (int e = threadIdx.x; e < E; e += kThreads) {
-    int pos = s_off[e];
-    if (s_cnt[e] > 0) {
-      for (int q = 0; q < P; ++q) {
-        if (s_e[q] != e) continue;
-        p.pair_tok[pos] = q / K;
-        p.pair_w[pos] = p.wts[q];
-        p.pidx[(q / K) * (K + 1) + q % K] = pos;
-        ++pos;
-      }
+    pairs = block_sum(pairs, s_red);
+    chunks = block_sum(chunks, s_red);
+    if (threadIdx.x == 0) {
+      p.hdr->n_pairs = pairs + (p.shared ? p.m : 0);
+      p.hdr->n_routed_chunks = chunks;
     }
-    for (int c = 0, ch = s_choff[e]; c < s_cnt[e]; c += kChunk, ++ch) {
-      p.chunk_e[ch] = e;
-      p.chunk_p0[ch] = s_off[e] + c;
-      p.chunk_n[ch] = min(kChunk, s_cnt[e] - c);
-    }
-  }
-  for (int t = threadIdx.x; t < p.m; t += kThreads) {
-    const int pos = s_off[E] + t;
-    if (p.shared) {
+    for (int q = threadIdx.x; q < P; q += kThreads)
+      if (s_e[q] < 0) p.pidx[(q / K) * (K + 1) + q % K] = -1;
+    for (int t = threadIdx.x; t < p.m; t += kThreads) {
+      const int pos = pairs + t;
+      p.pidx[t * (K + 1) + K] = p.shared ? pos : -1;
+      if (!p.shared) continue;
       p.pair_tok[pos] = t;
       p.pair_w[pos] = 1.0f;
+      if (t % kChunk == 0) {
+        const int ch = chunks + t / kChunk;
+        p.chunk_e[ch] = E;
+        p.chunk_p0[ch] = pos;
+        p.chunk_n[ch] = min(kChunk, p.m - t);
+      }
     }
-    p.pidx[t * (K + 1) + K] = p.shared ? pos : -1;
-    if (p.shared && t % kChunk == 0) {
-      const int ch = s_choff[E] + t / kChunk;
-      p.chunk_e[ch] = E;
-      p.chunk_p0[ch] = pos;
-      p.chunk_n[ch] = min(kChunk, p.m - t);
+    return;
+  }
+  const int cnt = s_cnt[me];
+  if (cnt == 0) return;  // uniform across the workgroup
+  int off = 0, choff = 0;
+  for (int e = threadIdx.x; e < me; e += kThreads) {
+    off += s_cnt[e];
+    choff += (s_cnt[e] + kChunk - 1) / kChunk;
+  }
+  off = block_sum(off, s_red);
+  choff = block_sum(choff, s_red);
+  int base = off;
+  for (int q0 = 0; q0 < P; q0 += kThreads) {
+    const int q = q0 + threadIdx.x;
+    const bool hit = q < P && s_e[q] == me;
+    const unsigned long long bal = __ballot(hit);
+    if (lane == 0) s_wc[wave] = __popcll(bal);
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) {
+      before += w < wave ? s_wc[w] : 0;
+      total += s_wc[w];
     }
+    if (hit) {
+      const int pos = base + before + __popcll(bal & ((1ull << lane) - 1ull));
+      p.pair_tok[pos] = q / K;
+      p.pair_w[pos] = p.wts[q];
+      p.pidx[(q / K) * (K + 1) + q % K] = pos;
+    }
+    base += total;
+    __syncthreads();
+  }
+  for (int c = threadIdx.x; c * kChunk < cnt; c += kThreads) {
+    p.chunk_e[choff + c] = me;
+    p.chunk_p0[choff + c] = off + c * kChunk;
+    p.chunk_n[choff + c] = min(kChunk, cnt - c * kChunk);
   }
 }
 
@@ -149,19 +187,6 @@ __global__ void __launch_bounds__(kThreads) prefill_group_kernel(PrefillParams p
 // lane (c, g) takes token tile*16 + c, columns 128*st + 32g + 8j .. +8.
 __device__ __forceinline__ bf16x8 tile_frag(const uint16_t* t, int cols, int tile, int c, int g, int st, int j) {
   return *reinterpret_cast<const bf16x8*>(t + (tile * 16 + c) * (cols + kPad) + st * 128 + g * 32 + 8 * j);
-}
-
-// Copies columns [c0, c0 + cols) of rows src_row(tt) (tt < n; zeros above) into
-// an LDS tile [kChunk][cols + kPad], 16 bytes per thread per pass.
-template <typename RowPtr>
-__device__ __forceinline__ void stage_rows(uint16_t* t, int cols, int n, RowPtr src_row) {
-  const int per_row = cols / 8;
-  for (int u = threadIdx.x; u < kChunk * per_row; u += kThreads) {
-    const int tt = u / per_row, cc = u - tt * per_row;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (tt < n) v = *reinterpret_cast<const uint4*>(src_row(tt) + cc * 8);
-    *reinterpret_cast<uint4*>(t + tt * (cols + kPad) + cc * 8) = v;
-  }
 }
 
 struct Chunk {
@@ -186,83 +211,143 @@ __device__ __forceinline__ bool load_chunk(const PrefillParams& p, int q, Chunk&
   return true;
 }
 
-// Software pipeline over weight batches of kB steps: the batch after the one
-// being multiplied is always in flight.  Step s of the stream is column block
-// 128 s .. 128 s + 127 of the weight rows; K-chunks of kSteps steps have their
-// token tile staged in LDS by stage(kc) (block-wide, between barriers) before
-// their batches are used.
-template <int F, int kB, int kSteps, int kMats, typename Stage, typename Mul>
-__device__ __forceinline__ void stream_rows(const uint64_t* ent, int w_slot, int64_t row, int64_t k, int g,
-                                            Stage&& stage, Mul&& mul) {
-  static_assert(kSteps % kB == 0, "batches must tile a K-chunk");
-  const int total = (int)(k / 128);
-  Batch<F, kB> n[kMats];
+// This thread's share of a token tile [kChunk][kCols] of kPlanes planes,
+// held in registers between its global loads and its LDS store.  Rows past
+// the chunk's n tokens are zero and never loaded.
+template <int kPlanes>
+struct XStage {
+  static constexpr int kPer = kChunk * kCols / 8 / kThreads;  // uint4 per thread and plane
+  uint4 v[kPlanes][kPer];
+  template <typename Src>
+  __device__ __forceinline__ void load(Src& src, int kc, int n) {
 #pragma unroll
-  for (int q = 0; q < kMats; ++q) n[q].load(ent[w_slot + 2 * q], ent[w_slot + 2 * q + 1], row, k, 0, g);
-  for (int kc = 0; kc * kSteps < total; ++kc) {
-    __syncthreads();
-    stage(kc);
-    __syncthreads();
+    for (int pl = 0; pl < kPlanes; ++pl)
 #pragma unroll
-    for (int sb = 0; sb < kSteps / kB; ++sb) {
-      Batch<F, kB> c[kMats];
-#pragma unroll
-      for (int q = 0; q < kMats; ++q) c[q] = n[q];
-      const int nxt = kc * kSteps + (sb + 1) * kB;
-      if (nxt < total) {
-#pragma unroll
-        for (int q = 0; q < kMats; ++q) n[q].load(ent[w_slot + 2 * q], ent[w_slot + 2 * q + 1], row, k, nxt, g);
+      for (int u = 0; u < kPer; ++u) {
+        const int q = threadIdx.x + u * kThreads, tt = q / (kCols / 8), cc = q % (kCols / 8);
+        v[pl][u] = tt < n ? ldg<uint4>(src(pl, tt) + kc * kCols + cc * 8) : make_uint4(0, 0, 0, 0);
       }
-      mul(c, sb * kB);
+  }
+  __device__ __forceinline__ void store(uint16_t* lds) const {
+#pragma unroll
+    for (int pl = 0; pl < kPlanes; ++pl)
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int q = threadIdx.x + u * kThreads, tt = q / (kCols / 8), cc = q % (kCols / 8);
+        *reinterpret_cast<uint4*>(lds + pl * kChunk * (kCols + kPad) + tt * (kCols + kPad) + cc * 8) = v[pl][u];
+      }
+  }
+};
+
+// The weights of one K-chunk for a wave: kMats matrices x kRT row tiles.
+template <int F, int kMats, int kRT>
+struct WBuf {
+  static constexpr int kSteps = kCols / 128;
+  Batch<F, kSteps> b[kMats][kRT];
+  __device__ __forceinline__ void load(const uint64_t* ent, int w_slot, int64_t row, int64_t k, int kc, int g) {
+#pragma unroll
+    for (int q = 0; q < kMats; ++q)
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt)
+        b[q][rt].load(ent[w_slot + 2 * q], ent[w_slot + 2 * q + 1], row + 16 * rt, k, kc * kSteps, g);
+  }
+};
+
+// Software pipeline over K-chunks.  While chunk kc is multiplied, the token
+// tile of kc + 1 is in flight to registers and the weights of kc + 2 to the
+// third weight buffer; the tile loads are issued before the weight loads.
+// Buffers rotate statically (three steps per loop turn).
+template <int F, int kMats, int kRT, int kPlanes, typename Src, typename Mul>
+__device__ __forceinline__ void pipeline(const uint64_t* ent, int w_slot, int64_t row, int64_t k, int g, int n,
+                                         uint16_t* lds, Src&& src, Mul&& mul) {
+  using W = WBuf<F, kMats, kRT>;
+  const int nkc = (int)(k / kCols);
+  XStage<kPlanes> xr;
+  if constexpr (F == kBf16) {
+    // bf16 weights (a compatibility format, 4x the bytes): one buffer, no
+    // weight prefetch, so that this path never raises the kernel's registers
+    W w;
+    for (int kc = 0; kc < nkc; ++kc) {
+      xr.load(src, kc, n);
+      w.load(ent, w_slot, row, k, kc, g);
+      __syncthreads();
+      xr.store(lds);
+      __syncthreads();
+      mul(w);
     }
+    return;
+  }
+  W w0, w1, w2;
+  xr.load(src, 0, n);
+  w0.load(ent, w_slot, row, k, 0, g);
+  if (nkc > 1) w1.load(ent, w_slot, row, k, 1, g);
+  auto step = [&](const W& wc, W& wl, int kc) {
+    __syncthreads();
+    xr.store(lds);
+    __syncthreads();
+    if (kc + 1 < nkc) xr.load(src, kc + 1, n);
+    if (kc + 2 < nkc) wl.load(ent, w_slot, row, k, kc + 2, g);
+    mul(wc);
+  };
+  for (int kc = 0; kc < nkc; kc += 3) {
+    step(w0, w2, kc);
+    if (kc + 1 < nkc) step(w1, w0, kc + 1);
+    if (kc + 2 < nkc) step(w2, w1, kc + 2);
   }
 }
 
 // ---------------------------------------------------------------- gate / up
-// Wave rows r0 .. r0+15 of W1 and W3 against the chunk's tokens; lane (r, g)
-// ends holding rows r0 + 4g + q of token tile*16 + r.
-template <int F, int kB>
+// Wave rows r0 .. r0+16*kGuRT-1 of W1 and W3 against the chunk's tokens; lane
+// (r, g) ends holding rows r0 + 16 rt + 4g + q of token tile*16 + r.
+template <int F>
 __device__ void gate_up_chunk(const PrefillParams& p, const Chunk& ch, int r0, uint16_t* xs, const int* s_tok) {
-  constexpr int kSteps = kGuCols / 128;
+  using W = WBuf<F, 2, kGuRT>;
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int ntile = (ch.n + 15) / 16;
-  f32x4 ag[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}}, au[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-  stream_rows<F, kB, kSteps, 2>(
-      ch.ent, 0, r0 + r, p.d, g,
-      [&](int kc) {
-        stage_rows(xs, kGuCols, ch.n, [&](int tt) { return p.x + (int64_t)s_tok[tt] * p.d + kc * kGuCols; });
-      },
-      [&](const Batch<F, kB>* w, int s0) {
+  f32x4 ag[kGuRT][2], au[kGuRT][2];
 #pragma unroll
-        for (int tile = 0; tile < 2; ++tile) {
-          if (tile >= ntile) break;
+  for (int rt = 0; rt < kGuRT; ++rt)
 #pragma unroll
-          for (int b = 0; b < kB; ++b) {
+    for (int t = 0; t < 2; ++t) ag[rt][t] = au[rt][t] = f32x4{0, 0, 0, 0};
+  auto src = [&](int, int tt) { return p.x + (int64_t)s_tok[tt] * p.d; };
+  pipeline<F, 2, kGuRT, 1>(ch.ent, 0, r0 + r, p.d, g, ch.n, xs, src, [&](const W& w) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const bf16x8 xf = tile_frag(xs, kGuCols, tile, r, g, s0 + b, j);
-              ag[tile] = mfma16x16x32(w[0].frag(b, j, g), xf, ag[tile]);
-              au[tile] = mfma16x16x32(w[1].frag(b, j, g), xf, au[tile]);
-            }
+    for (int b = 0; b < W::kSteps; ++b) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int rt = 0; rt < kGuRT; ++rt) {
+          const bf16x8 f1 = w.b[0][rt].frag(b, j, g), f3 = w.b[1][rt].frag(b, j, g);
+#pragma unroll
+          for (int tile = 0; tile < 2; ++tile) {
+            if (tile >= ntile) break;
+            const bf16x8 xf = tile_frag(xs, kCols, tile, r, g, b, j);
+            ag[rt][tile] = mfma16x16x32(f1, xf, ag[rt][tile]);
+            au[rt][tile] = mfma16x16x32(f3, xf, au[rt][tile]);
           }
         }
-      });
+      }
+    }
+  });
 #pragma unroll
   for (int tile = 0; tile < 2; ++tile) {
     const int tt = tile * 16 + r;
     if (tile >= ntile || tt >= ch.n) continue;
     const int64_t pr = ch.p0 + tt;
     const float wt = p.pair_w[pr];
-    uint32_t hi[4], lo[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float a = __fmul_rn(wt, swiglu(ag[tile][q], au[tile][q], p.limit));
-      hi[q] = f32_to_bf16_bits(a);
-      lo[q] = f32_to_bf16_bits(__fadd_rn(a, -bf16_bits_to_f32(hi[q])));
+    for (int rt = 0; rt < kGuRT; ++rt) {
+      uint32_t hi[4], lo[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a = __fmul_rn(wt, swiglu(ag[rt][tile][q], au[rt][tile][q], p.limit));
+        hi[q] = f32_to_bf16_bits(a);
+        lo[q] = f32_to_bf16_bits(__fadd_rn(a, -bf16_bits_to_f32(hi[q])));
+      }
+      const int64_t o = pr * p.i + r0 + 16 * rt + 4 * g;
+      *reinterpret_cast<uint2*>(p.act_hi + o) = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
+      *reinterpret_cast<uint2*>(p.act_lo + o) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
     }
-    const int64_t o = pr * p.i + r0 + 4 * g;
-    *reinterpret_cast<uint2*>(p.act_hi + o) = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
-    *reinterpret_cast<uint2*>(p.act_lo + o) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
   }
 }
 
@@ -270,64 +355,70 @@ __device__ void gate_up_chunk(const PrefillParams& p, const Chunk& ch, int r0, u
 // the shared expert's FP8); table entries without scales take the bf16 path.
 template <int F, bool kShared>
 __global__ void __launch_bounds__(kThreads) prefill_gate_up_kernel(PrefillParams p) {
-  __shared__ __align__(16) uint16_t xs[kChunk * (kGuCols + kPad)];
+  __shared__ __align__(16) uint16_t xs[kChunk * (kCols + kPad)];
   __shared__ int s_tok[kChunk];
-  const int nrb = p.i / kRows;
+  const int nrb = p.i / kGuRows;
   Chunk ch;
   if (!load_chunk<kShared>(p, blockIdx.x / nrb, ch)) return;
   if (threadIdx.x < kChunk) s_tok[threadIdx.x] = threadIdx.x < ch.n ? p.pair_tok[ch.p0 + threadIdx.x] : 0;
-  const int r0 = (blockIdx.x % nrb) * kRows + 16 * (threadIdx.x >> 6);
-  if (ch.ent[1]) gate_up_chunk<F, (F == kFp8Block ? 2 : 4)>(p, ch, r0, xs, s_tok);
-  else gate_up_chunk<kBf16, 1>(p, ch, r0, xs, s_tok);
+  __syncthreads();
+  const int r0 = (blockIdx.x % nrb) * kGuRows + 16 * kGuRT * (threadIdx.x >> 6);
+  if (ch.ent[1]) gate_up_chunk<F>(p, ch, r0, xs, s_tok);
+  else gate_up_chunk<kBf16>(p, ch, r0, xs, s_tok);
 }
 
 // ---------------------------------------------------------------- down
-template <int F, int kB>
-__device__ void down_chunk(const PrefillParams& p, const Chunk& ch, int r0, uint16_t* hs, uint16_t* ls) {
-  constexpr int kSteps = kDnCols / 128;
+template <int F>
+__device__ void down_chunk(const PrefillParams& p, const Chunk& ch, int r0, uint16_t* as) {
+  using W = WBuf<F, 1, kDnRT>;
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int ntile = (ch.n + 15) / 16;
-  f32x4 acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-  stream_rows<F, kB, kSteps, 1>(
-      ch.ent, 4, r0 + r, p.i, g,
-      [&](int kc) {
-        stage_rows(hs, kDnCols, ch.n, [&](int tt) { return p.act_hi + (int64_t)(ch.p0 + tt) * p.i + kc * kDnCols; });
-        stage_rows(ls, kDnCols, ch.n, [&](int tt) { return p.act_lo + (int64_t)(ch.p0 + tt) * p.i + kc * kDnCols; });
-      },
-      [&](const Batch<F, kB>* w, int s0) {
+  const uint16_t* ls = as + kChunk * (kCols + kPad);
+  f32x4 acc[kDnRT][2];
+#pragma unroll
+  for (int rt = 0; rt < kDnRT; ++rt) acc[rt][0] = acc[rt][1] = f32x4{0, 0, 0, 0};
+  auto src = [&](int pl, int tt) { return (pl ? p.act_lo : p.act_hi) + (int64_t)(ch.p0 + tt) * p.i; };
+  pipeline<F, 1, kDnRT, 2>(ch.ent, 4, r0 + r, p.i, g, ch.n, as, src, [&](const W& w) {
+#pragma unroll
+    for (int b = 0; b < W::kSteps; ++b) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
 #pragma unroll
         for (int tile = 0; tile < 2; ++tile) {
           if (tile >= ntile) break;
+          const bf16x8 hf = tile_frag(as, kCols, tile, r, g, b, j), lf = tile_frag(ls, kCols, tile, r, g, b, j);
 #pragma unroll
-          for (int b = 0; b < kB; ++b) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const bf16x8 wf = w[0].frag(b, j, g);
-              acc[tile] = mfma16x16x32(wf, tile_frag(hs, kDnCols, tile, r, g, s0 + b, j), acc[tile]);
-              acc[tile] = mfma16x16x32(wf, tile_frag(ls, kDnCols, tile, r, g, s0 + b, j), acc[tile]);
-            }
+          for (int rt = 0; rt < kDnRT; ++rt) {
+            const bf16x8 wf = w.b[0][rt].frag(b, j, g);
+            acc[rt][tile] = mfma16x16x32(wf, hf, acc[rt][tile]);
+            acc[rt][tile] = mfma16x16x32(wf, lf, acc[rt][tile]);
           }
         }
-      });
+      }
+    }
+  });
 #pragma unroll
   for (int tile = 0; tile < 2; ++tile) {
     const int tt = tile * 16 + r;
     if (tile >= ntile || tt >= ch.n) continue;
-    float* o = p.part + (int64_t)(ch.p0 + tt) * p.d + r0 + 4 * g;
-    *reinterpret_cast<float4*>(o) = make_float4(acc[tile][0], acc[tile][1], acc[tile][2], acc[tile][3]);
+#pragma unroll
+    for (int rt = 0; rt < kDnRT; ++rt) {
+      float* o = p.part + (int64_t)(ch.p0 + tt) * p.d + r0 + 16 * rt + 4 * g;
+      *reinterpret_cast<float4*>(o) = make_float4(acc[rt][tile][0], acc[rt][tile][1], acc[rt][tile][2], acc[rt][tile][3]);
+    }
   }
 }
 
 template <int F, bool kShared>
-__global__ void __launch_bounds__(kThreads) prefill_down_kernel(PrefillParams p) {
-  __shared__ __align__(16) uint16_t hs[kChunk * (kDnCols + kPad)];
-  __shared__ __align__(16) uint16_t ls[kChunk * (kDnCols + kPad)];
-  const int nrb = p.d / kRows;
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(F == kFp8Block ? 2 : 3)))
+prefill_down_kernel(PrefillParams p) {
+  __shared__ __align__(16) uint16_t as[2 * kChunk * (kCols + kPad)];  // hi plane, lo plane
+  const int nrb = p.d / kDnRows;
   Chunk ch;
   if (!load_chunk<kShared>(p, blockIdx.x / nrb, ch)) return;
-  const int r0 = (blockIdx.x % nrb) * kRows + 16 * (threadIdx.x >> 6);
-  if (ch.ent[1]) down_chunk<F, 2>(p, ch, r0, hs, ls);
-  else down_chunk<kBf16, 1>(p, ch, r0, hs, ls);
+  const int r0 = (blockIdx.x % nrb) * kDnRows + 16 * kDnRT * (threadIdx.x >> 6);
+  if (ch.ent[1]) down_chunk<F>(p, ch, r0, as);
+  else down_chunk<kBf16>(p, ch, r0, as);
 }
 
 // ---------------------------------------------------------------- combine
@@ -458,22 +549,22 @@ extern "C" int hsmoe_moe_prefill(const void* x, int64_t m, int64_t d, int64_t i,
   p.limit = swiglu_limit;
   hipStream_t st = (hipStream_t)stream;
   const int64_t C = max_routed_chunks(m, n_experts, top_k), CS = shared ? (m + kChunk - 1) / kChunk : 0;
-  hipLaunchKernelGGL(prefill_group_kernel, dim3(1), dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL(prefill_group_kernel, dim3((unsigned)n_experts + 1), dim3(kThreads), 0, st, p);
   int rc = check_launch(name);
   if (rc) return rc;
-  const dim3 blk(kThreads), gu((unsigned)(C * (i / kRows))), dn((unsigned)(C * (d / kRows)));
+  const dim3 blk(kThreads), gu((unsigned)(C * (i / kGuRows))), dn((unsigned)(C * (d / kDnRows)));
   if (scale_kind == HSMOE_SCALE_E8M0) hipLaunchKernelGGL((prefill_gate_up_kernel<kFp4E8M0, false>), gu, blk, 0, st, p);
   else hipLaunchKernelGGL((prefill_gate_up_kernel<kFp4F32, false>), gu, blk, 0, st, p);
   if ((rc = check_launch(name))) return rc;
   if (CS) {
-    hipLaunchKernelGGL((prefill_gate_up_kernel<kFp8Block, true>), dim3((unsigned)(CS * (i / kRows))), blk, 0, st, p);
+    hipLaunchKernelGGL((prefill_gate_up_kernel<kFp8Block, true>), dim3((unsigned)(CS * (i / kGuRows))), blk, 0, st, p);
     if ((rc = check_launch(name))) return rc;
   }
   if (scale_kind == HSMOE_SCALE_E8M0) hipLaunchKernelGGL((prefill_down_kernel<kFp4E8M0, false>), dn, blk, 0, st, p);
   else hipLaunchKernelGGL((prefill_down_kernel<kFp4F32, false>), dn, blk, 0, st, p);
   if ((rc = check_launch(name))) return rc;
   if (CS) {
-    hipLaunchKernelGGL((prefill_down_kernel<kFp8Block, true>), dim3((unsigned)(CS * (d / kRows))), blk, 0, st, p);
+    hipLaunchKernelGGL((prefill_down_kernel<kFp8Block, true>), dim3((unsigned)(CS * (d / kDnRows))), blk, 0, st, p);
     if ((rc = check_launch(name))) return rc;
   }
   hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)m, (unsigned)(d / (4 * kThreads))), dim3(kThreads), 0,

@@ -29,14 +29,14 @@ struct Batch<kFp4E8M0, kB> {
   __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
     const uint8_t* base = (const uint8_t*)w + row * (k / 2) + st * 64 + g * 16;
 #pragma unroll
-    for (int b = 0; b < kB; ++b) a[b] = *reinterpret_cast<const uint4*>(base + b * 64);
+    for (int b = 0; b < kB; ++b) a[b] = ldg<uint4>(base + b * 64);
     const uint8_t* sp = (const uint8_t*)sc + row * (k / 32) + st * 4;
     if constexpr (kB >= 4) {
 #pragma unroll
-      for (int q = 0; q < kB / 4; ++q) sq[q] = *reinterpret_cast<const uint4*>(sp + 16 * q);
+      for (int q = 0; q < kB / 4; ++q) sq[q] = ldg<uint4>(sp + 16 * q);
     } else {
 #pragma unroll
-      for (int b = 0; b < kB; ++b) sb[b] = sp[4 * b + g];
+      for (int b = 0; b < kB; ++b) sb[b] = ldg<uint8_t>(sp + 4 * b + g);
     }
   }
   __device__ __forceinline__ bf16x8 frag(int b, int j, int g) const {
@@ -64,8 +64,8 @@ struct Batch<kFp4F32, kB> {
     const float* sp = (const float*)sc + row * (k / 32) + st * 4 + g;
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
-      a[b] = *reinterpret_cast<const uint4*>(base + b * 64);
-      s[b] = sp[4 * b];
+      a[b] = ldg<uint4>(base + b * 64);
+      s[b] = ldg<float>(sp + 4 * b);
     }
   }
   __device__ __forceinline__ bf16x8 frag(int b, int j, int) const {
@@ -84,9 +84,9 @@ struct Batch<kFp8Block, kB> {
     const float* sp = (const float*)sc + (row / 128) * (k / 128) + st;
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
-      a[b] = *reinterpret_cast<const uint4*>(base + b * 128);
-      c[b] = *reinterpret_cast<const uint4*>(base + b * 128 + 16);
-      s[b] = sp[b];
+      a[b] = ldg<uint4>(base + b * 128);
+      c[b] = ldg<uint4>(base + b * 128 + 16);
+      s[b] = ldg<float>(sp + b);
     }
   }
   __device__ __forceinline__ bf16x8 frag(int b, int j, int) const {
@@ -107,7 +107,7 @@ struct Batch<kBf16, kB> {
 #pragma unroll
     for (int b = 0; b < kB; ++b)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) a[b][j] = base[b * 16 + j];
+      for (int j = 0; j < 4; ++j) a[b][j] = ldg<uint4>(base + b * 16 + j);
   }
   __device__ __forceinline__ bf16x8 frag(int b, int j, int) const { return __builtin_bit_cast(bf16x8, a[b][j]); }
 };

@@ -169,7 +169,7 @@ def moe_decode(x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor, ta
     return out_bf16, out_f32
 
 
-MAX_PREFILL_PAIRS = 16384  # m * top_k per hsmoe_moe_prefill call
+MAX_PREFILL_PAIRS = 12288  # m * top_k per hsmoe_moe_prefill call
 
 
 def moe_prefill(x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor, table: torch.Tensor,

@@ -177,7 +177,7 @@ size_t hsmoe_moe_layer_status_offset(void);
  * then + shared FFN(x[t]); a (t, j) with an invalid id or absent expert adds
  * nothing.  Each selected expert's weights are read once per chunk of up to
  * 32 of its tokens.  Deterministic (no atomics).
- * 1 <= m * top_k <= 16384, n_experts <= 1024, top_k <= 16, d % 1024 == 0,
+ * 1 <= m * top_k <= 12288, n_experts <= 1024, top_k <= 16, d % 1024 == 0,
  * i % 512 == 0; x and out_f32 16-byte aligned, out_bf16 8-byte aligned.
  * The workspace (any contents) must hold hsmoe_moe_prefill_workspace_size bytes. */
 size_t hsmoe_moe_prefill_workspace_size(int64_t m, int64_t d, int64_t i, int64_t n_experts, int top_k);
