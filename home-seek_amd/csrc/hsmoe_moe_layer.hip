@@ -249,8 +249,7 @@ __device__ __forceinline__ void ensure_x(const LayerParams& p, int& state) {
   for (int q0 = threadIdx.x; q0 < n16; q0 += 8 * kThreads) {
     uint4 v[8];  // every load of the pass in flight before the first LDS store
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (q0 + j * kThreads < n16) v[j] = src[q0 + j * kThreads];
+    for (int j = 0; j < 8; ++j) v[j] = q0 + j * kThreads < n16 ? src[q0 + j * kThreads] : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       if (q0 + j * kThreads < n16) reinterpret_cast<uint4*>(g_tile)[q0 + j * kThreads] = v[j];
