@@ -216,10 +216,11 @@ __device__ __forceinline__ void write_routing(const LayerParams& p, Shared& sh) 
 extern __shared__ __align__(16) uint16_t g_tile[];
 __shared__ Shared g_sh;
 
-// The item functions are not inlined (each keeps its own register budget), so
-// they read the launch parameters through the kernel's kernarg-segment address,
-// which the kernel passes down: that builtin yields a valid address only in
-// the kernel itself.
+// The streaming item functions are not inlined (each keeps its own register
+// budget), so they read the launch parameters through the kernel's
+// kernarg-segment address, which the kernel passes down: that builtin yields a
+// valid address only in the kernel itself.  The router item is inlined: as a
+// call it had to save a callee-saved register to scratch.
 typedef const __attribute__((address_space(4))) LayerParams KernargParams;
 
 __device__ __forceinline__ LayerParams params(uint64_t kernarg) {
@@ -258,7 +259,7 @@ __device__ __forceinline__ void ensure_x(const LayerParams& p, int& state) {
   state = 1;
 }
 
-__device__ __noinline__ int router_item(uint64_t kernarg, int q_arg, int state_arg) {
+__device__ __forceinline__ int router_item(uint64_t kernarg, int q_arg, int state_arg) {
   const int q = __builtin_amdgcn_readfirstlane(q_arg);
   int state = __builtin_amdgcn_readfirstlane(state_arg);
   const LayerParams p = params(kernarg);

@@ -141,46 +141,38 @@ __device__ __forceinline__ void router_row(const uint4 (&wv)[kMaxChunks], const 
                                            int64_t e, int64_t n_exp, const float* bias, uint16_t* logits_row,
                                            float* scores) {
   const int lane = threadIdx.x & 63;
-  double acc[kRouterTok];
+  float b = 0.0f;
+  if (bias) b = bf16_bits_to_f32(f32_to_bf16_bits(bias[e]));
+  // One token at a time (a rolled loop: the unrolled token loop made this the
+  // largest straight-line code of the layer kernel, fetched cold by every
+  // router item); per token the sum runs over chunks, then words, in order.
+#pragma unroll 1
+  for (int t = 0; t < nt; ++t) {
+    double acc = 0.0;
 #pragma unroll
-  for (int t = 0; t < kRouterTok; ++t) acc[t] = 0.0;
+    for (int c = 0; c < kMaxChunks; ++c) {
+      if (lane * 8 + 512 * c < d) {
+        uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+        // opaque to the optimiser: the fp64 weights are rebuilt per token
+        // instead of being hoisted out of the token loop (256 registers)
+        asm volatile("" : "+v"(ww[0]), "+v"(ww[1]), "+v"(ww[2]), "+v"(ww[3]));
+        const uint4 xv = *reinterpret_cast<const uint4*>(xs + t * d + lane * 8 + 512 * c);
+        const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
-    if (lane * 8 + 512 * c < d) {
-      const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
-      double wd[8];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        wd[2 * q] = (double)__uint_as_float(ww[q] << 16);
-        wd[2 * q + 1] = (double)__uint_as_float(ww[q] & 0xffff0000u);
-      }
-#pragma unroll
-      for (int t = 0; t < kRouterTok; ++t) {
-        if (t < nt) {
-          const uint4 xv = *reinterpret_cast<const uint4*>(xs + t * d + lane * 8 + 512 * c);
-          const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            acc[t] = __fma_rn((double)__uint_as_float(xx[q] << 16), wd[2 * q], acc[t]);
-            acc[t] = __fma_rn((double)__uint_as_float(xx[q] & 0xffff0000u), wd[2 * q + 1], acc[t]);
-          }
+        for (int q = 0; q < 4; ++q) {
+          acc = __fma_rn((double)__uint_as_float(xx[q] << 16), (double)__uint_as_float(ww[q] << 16), acc);
+          acc = __fma_rn((double)__uint_as_float(xx[q] & 0xffff0000u), (double)__uint_as_float(ww[q] & 0xffff0000u),
+                         acc);
         }
       }
     }
-  }
-  float b = 0.0f;
-  if (bias) b = bf16_bits_to_f32(f32_to_bf16_bits(bias[e]));
-#pragma unroll
-  for (int t = 0; t < kRouterTok; ++t) {
-    if (t < nt) {
-      const double sum = wave_sum_f64(acc[t]);
-      if (lane == 0) {
-        uint32_t l = f64_to_bf16_bits(sum);
-        if (bias) l = f32_to_bf16_bits(__fadd_rn(bf16_bits_to_f32(l), b));
-        if (logits_row) logits_row[t * n_exp] = (uint16_t)l;
-        const float score = sqrtf(softplus_f32(bf16_bits_to_f32(l)));
-        __hip_atomic_store(scores + t * n_exp, score, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+    const double sum = wave_sum_f64(acc);
+    if (lane == 0) {
+      uint32_t l = f64_to_bf16_bits(sum);
+      if (bias) l = f32_to_bf16_bits(__fadd_rn(bf16_bits_to_f32(l), b));
+      if (logits_row) logits_row[t * n_exp] = (uint16_t)l;
+      const float score = sqrtf(softplus_f32(bf16_bits_to_f32(l)));
+      __hip_atomic_store(scores + t * n_exp, score, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
