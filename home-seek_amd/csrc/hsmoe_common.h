@@ -41,6 +41,30 @@ __device__ __forceinline__ uint4 ldg<uint4>(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// A buffer resource (V#) over `bytes` bytes at `base`: loads through it take a
+// 32-bit per-lane offset plus an immediate (one offset register serves a whole
+// batch of loads), and a load past `bytes` returns zeros instead of touching
+// memory.  base is made wave-uniform (it lives in scalar registers).
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+__device__ __forceinline__ BufRsrc make_buf(uint64_t base, uint32_t bytes) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+  const uint32_t n = __builtin_amdgcn_readfirstlane(bytes);
+  // word 3 = 0x00020000: raw (unformatted) 32-bit data, the gfx9 setting
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, (int)n, 0x00020000);
+}
+__device__ __forceinline__ uint4 bload128(BufRsrc r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t bload32(BufRsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ float bloadf(BufRsrc r, uint32_t off) { return __uint_as_float(bload32(r, off)); }
+__device__ __forceinline__ uint32_t bload8(BufRsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
+}
+
 // ------------------------------------------------------------------ bits
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 

@@ -15,4 +15,8 @@ int check_launch(const char* what);
 
 inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// Expert weights are read through buffer resources with 32-bit offsets: an
+// expert matrix (d x i, up to 2 bytes per element) must stay below 4 GiB.
+inline bool expert_fits(int64_t d, int64_t i) { return (uint64_t)d * (uint64_t)i * 2 < (1ull << 32); }
+
 }  // namespace hsmoe

@@ -121,7 +121,7 @@ __global__ void __launch_bounds__(64 * kP1Waves) moe_gate_up_kernel(DecodeParams
   const int per = (p.d / 128) / kP1Waves;
   const int st0 = wave * per, st1 = st0 + per;
   f32x4 ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
-  gate_up_slot(slot_format(p.scale_fmt, ent, is_shared), ent, xs, p.m, p.d, r0, st0, st1, ag, au);
+  gate_up_slot(slot_format(p.scale_fmt, ent, is_shared), ent, xs, p.m, p.d, p.i, r0, st0, st1, ag, au);
   // D[4*(lane/16) + q][lane%16] lives in element q of lane
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -189,7 +189,7 @@ __global__ void __launch_bounds__(64 * kP2Waves) moe_down_kernel(DecodeParams p)
   f32x4 acc = {0, 0, 0, 0};
   // the W2 rows do not depend on the activations: their first batch is in
   // flight while the tile is staged
-  down_slot(slot_format(p.scale_fmt, ent, is_shared), ent, as, p.m, p.i, r0, acc, [&]() {
+  down_slot(slot_format(p.scale_fmt, ent, is_shared), ent, as, p.m, p.i, p.d, r0, acc, [&]() {
     for (int q = threadIdx.x; q < n16; q += blockDim.x) reinterpret_cast<uint4*>(as)[q] = src[q];
     __syncthreads();
   });
@@ -259,6 +259,8 @@ static int moe_decode_launch(const void* x, int64_t m, int64_t d, int64_t i, con
   if (d % 512 != 0 || i % 512 != 0 || d <= 0 || i <= 0 || (size_t)(d / 64) * 4 > kCounterBytes)
     return fail(HSMOE_ERR_SHAPE, "%s: d and i must be positive multiples of 512, d <= 65536 (d=%lld i=%lld)", name,
                 (long long)d, (long long)i);
+  if (!expert_fits(d, i))
+    return fail(HSMOE_ERR_SHAPE, "%s: d*i too large (an expert matrix must stay below 4 GiB)", name);
   if (!aligned(x, 16)) return fail(HSMOE_ERR_SHAPE, "%s: x must be 16-byte aligned", name);
   const size_t need = hsmoe_moe_decode_workspace_size(m, d, i, top_k);
   if (!workspace || workspace_bytes < need || !aligned(workspace, 256))

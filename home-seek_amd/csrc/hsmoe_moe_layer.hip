@@ -10,19 +10,22 @@
 // accumulation order), so the results are bit-identical to those two calls.
 //
 // Work items, in dependency order (item q only ever waits on items < q):
-//   R    router rows: 4 expert rows per item (one per wave), published as
-//        fp32 scores; the last R item to finish also writes the routing
-//        outputs (top-k ids and weights)
+//   R    router rows: one expert row per item (its columns spread over the
+//        workgroup's 256 threads), published as fp32 scores; the last R item
+//        to finish also writes the routing outputs (top-k ids and weights)
 //   SGU  shared-expert gate/up, 16 rows of W1 and W3 per item
 //   SD   shared-expert down, 64 rows of W2 per item (ahead of the routed
 //        items: its weights stream while the routing is still being decided)
 //   GU   routed gate/up, (slot, 16 rows) per item; needs the slot plan
 //   D    routed down, (slot, 64 rows) per item
-// Every workgroup that runs a routed item (or the shared down) first builds the
-// slot plan itself, once per launch, in LDS: it waits for all R items, loads
-// the scores, runs the top-k of every token and lists the distinct valid
-// expert ids ascending with their per-token weights (the same deterministic
-// computation in every workgroup, so all plans agree).
+// The last R item to finish builds the slot plan: top-k of every token from
+// the scores, then the distinct valid expert ids ascending with their
+// per-token weights.  It publishes the plan (expert id and weights per slot)
+// in kFlagCopies copies and then the router flag; every other workgroup that
+// runs a routed item (or the shared down) waits for the flag once per launch
+// and copies its copy of the plan into LDS.  R items count their arrivals in
+// groups of kRouterGroup (one counter per group, then one for the groups), so
+// no counter takes more than 16 atomic increments.
 // A down item issues its first W2 loads, then waits until every gate/up item
 // of its slot has published the slot's activations, then stages them in LDS.
 // The last down item of a row group adds the slots' partials in slot order
@@ -49,6 +52,7 @@ constexpr int kMaxSlots = 128;  // m * top_k routed slots; slot kMaxSlots is nev
 constexpr int kMaxExperts = 256;
 constexpr int kGuRows = 16;
 constexpr int kDownRows = 16 * kWaves;
+constexpr int kRtChunks = 8192 / 8 / kThreads;  // 16-byte gate-row chunks per thread (d <= 8192)
 constexpr unsigned kSpinLimit = 1u << 16;
 // Off: the launch faulted the GPU on MI355X (first with the parameters read
 // through a null kernarg pointer in the item functions, then once more after
@@ -66,13 +70,21 @@ constexpr int kCtlErr = 192;     // sticky: 1 + index of a control word whose wa
 constexpr int kCtlSlot = 256;    // + 16*s: gate/up items of slot s finished
 constexpr int kCtlRowGroup = kCtlSlot + 16 * (kMaxSlots + 1);  // + g: down items of row group g finished
 constexpr int kMaxRowGroups = 2048;
+constexpr int kCtlRouterGrp = 4608;  // + 64*g: router items of group g finished
+constexpr int kRouterGroup = 16;     // router items per group counter (at most 16 groups)
 constexpr int kFlagCopies = 8;
 constexpr int kFlagBase = 8192;      // word index of flag copy 0 (32 KiB)
 constexpr int kFlagStride = 1024;    // words between copies (4 KiB)
 constexpr int kFlagRouter = 0;       // + copy: every router item finished
 constexpr int kFlagSlot = 16;        // + 4*s: every gate/up item of slot s finished
 constexpr size_t kCtlBytes = 65536;
-static_assert(kCtlRowGroup + kMaxRowGroups <= kFlagBase, "control block overflow");
+static_assert(kCtlRowGroup + kMaxRowGroups <= kCtlRouterGrp, "control block overflow");
+static_assert(kCtlRouterGrp + 64 * (kMaxExperts / kRouterGroup) <= kFlagBase, "control block overflow");
+// Published plan, one copy per flag copy: [0] slot count, [1 + s] expert id of
+// slot s, [1 + S + s*m + t] weight of slot s for token t (S = m * top_k).
+constexpr int kPlanStride = 2048;  // words between copies (8 KiB)
+constexpr size_t kPlanBytes = (size_t)kFlagCopies * kPlanStride * 4;
+static_assert(1 + kMaxSlots + kMaxSlots * kMaxTok <= kPlanStride, "plan copy overflow");
 static_assert(kFlagSlot + 4 * (kMaxSlots + 1) <= kFlagStride, "flag block overflow");
 static_assert((kFlagBase + kFlagCopies * kFlagStride) * 4 <= (int)kCtlBytes, "flag copies overflow");
 
@@ -91,6 +103,7 @@ struct LayerParams {
   float* out_f32;      // [m, d] or null
   uint16_t* out_bf16;  // [m, d] or null
   unsigned* ctl;
+  unsigned* plan;  // kFlagCopies published slot plans
   float* scores;  // [m][n_exp]
   float* act;   // fp32 [S + 1][m][i] weighted activations (slot S = shared)
   float* part;  // fp32 [S + 1][m][d] per-slot down partials
@@ -122,6 +135,7 @@ __device__ __forceinline__ void set_flag(unsigned* ctl, int flag) {
 
 struct Shared {
   float red[kWaves][2][256];
+  double rpart[kWaves][kMaxTok];  // router: per-wave partial logit sums
   int64_t idx[kMaxSlots];  // top-k ids of every token
   float w[kMaxSlots];      // top-k weights of every token
   int eid[kMaxSlots];            // slot plan: expert id of routed slot s
@@ -131,21 +145,21 @@ struct Shared {
   int n_routed;
   int have_plan;
   int wave_count[kWaves];
-  unsigned char valid[kMaxExperts];  // expert e has a table entry (filled at kernel start)
+  unsigned char valid[kMaxExperts];  // expert e has a table entry (router items fill it)
   unsigned char used[kMaxExperts];   // expert e is selected by some token (plan build)
   short rank[kMaxExperts];           // slot of a selected expert (plan build)
 };
 
-// The slot plan of this launch in LDS, built once per workgroup: waits for
-// every router item, then top-k of every token (one token per wave, ties to
+// The slot plan of this launch in LDS, built by the last router item (every
+// score is published): top-k of every token (one token per wave, ties to
 // the lower index) and the distinct valid expert ids in ascending order with
 // each token's weight for them (its top-k weights for that id, summed in k
 // order; the union of _forward_legacy, fused_moe.py:466-476).
 __device__ __forceinline__ void build_plan(const LayerParams& p, Shared& sh) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = p.m * p.top_k;
+  // (sh.valid was filled by this workgroup's router item)
   for (int e = threadIdx.x; e < p.n_exp; e += kThreads) sh.used[e] = 0;
-  if (threadIdx.x == 0) wait_flag(p.ctl, kFlagRouter);
   __syncthreads();
   // (n_exp <= kMaxExperts: at most 4 keys per lane)
   for (int t = wave; t < p.m; t += kWaves) {
@@ -233,13 +247,42 @@ __device__ __forceinline__ LayerParams params(uint64_t kernarg) {
 #endif
 }
 
-// Builds the slot plan into g_sh (a function of its own, called from the
-// kernel's item loop, so the top-k state adds to no streaming item's
-// registers); the last router item also writes the routing outputs.
-__device__ __noinline__ void plan_item(uint64_t kernarg, int write_outputs) {
+// The slot plan in g_sh (a function of its own, called from the kernel's item
+// loop, so its state adds to no streaming item's registers).  The last router
+// item (publish) builds it, writes the routing outputs, publishes the plan
+// copies and then sets the router flag; every other workgroup waits for the
+// flag and copies the plan from copy blockIdx.x % kFlagCopies.
+__device__ __noinline__ void plan_item(uint64_t kernarg, int publish) {
   const LayerParams p = params(kernarg);
-  build_plan(p, g_sh);
-  if (__builtin_amdgcn_readfirstlane(write_outputs)) write_routing(p, g_sh);
+  Shared& sh = g_sh;
+  const int S = p.S, m = p.m, words = 1 + S + S * m;
+  if (__builtin_amdgcn_readfirstlane(publish)) {
+    build_plan(p, sh);
+    for (int k = threadIdx.x; k < words; k += kThreads) {
+      unsigned v;
+      if (k == 0) v = (unsigned)sh.n_routed;
+      else if (k <= S) v = (unsigned)sh.eid[k - 1];
+      else v = __float_as_uint(sh.wt[(k - 1 - S) / m][(k - 1 - S) % m]);
+#pragma unroll
+      for (int c = 0; c < kFlagCopies; ++c) store_agent(p.plan + c * kPlanStride + k, v);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) set_flag(p.ctl, kFlagRouter);
+    write_routing(p, sh);  // read only after the launch
+    return;
+  }
+  if (threadIdx.x == 0) wait_flag(p.ctl, kFlagRouter);
+  __syncthreads();
+  const unsigned* src = p.plan + (int)(blockIdx.x % kFlagCopies) * kPlanStride;
+  for (int k = threadIdx.x; k < words; k += kThreads) {
+    const unsigned v = load_agent(src + k);
+    if (k == 0) sh.n_routed = (int)v;
+    else if (k <= S) sh.eid[k - 1] = (int)v;
+    else sh.wt[(k - 1 - S) / m][(k - 1 - S) % m] = __uint_as_float(v);
+  }
+  if (threadIdx.x == 0) sh.have_plan = 1;
+  __syncthreads();
 }
 
 // Copies x into the LDS tile unless it is already there (state: 1 = x in LDS).
@@ -259,23 +302,60 @@ __device__ __forceinline__ void ensure_x(const LayerParams& p, int& state) {
   state = 1;
 }
 
+// Router row e = q: thread t owns the row's 16-byte chunks t, t + 256, ...;
+// per token it adds its exact products in fp64 (chunk then element order),
+// the wave sums by a fixed butterfly and the 4 wave sums are added in wave
+// order.  Every addition is of fp64 values holding exact bf16 products, so
+// for the rows met in practice the sum is exact and equals the column-order
+// sum; it is rounded to bf16 once.
 __device__ __forceinline__ int router_item(uint64_t kernarg, int q_arg, int state_arg) {
   const int q = __builtin_amdgcn_readfirstlane(q_arg);
   int state = __builtin_amdgcn_readfirstlane(state_arg);
   const LayerParams p = params(kernarg);
   Shared& sh = g_sh;
-  const int wave = threadIdx.x >> 6;
-  const int64_t e = (int64_t)q * kWaves + wave;
-  uint4 wv[kMaxChunks];
-  if (e < p.n_exp) load_gate_row(p.gate_w, e, p.d, wv);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t e = q;
+  const int nch = p.d / 8;
+  const uint4* wrow = reinterpret_cast<const uint4*>(p.gate_w + e * p.d);
+  uint4 wv[kRtChunks];
+#pragma unroll
+  for (int j = 0; j < kRtChunks; ++j) {
+    const int c = threadIdx.x + kThreads * j;
+    wv[j] = c < nch ? ldg<uint4>(wrow + c) : make_uint4(0, 0, 0, 0);
+  }
+  // which experts the table holds (used if this item turns out to be the last)
+  const bool has_entry = threadIdx.x < p.n_exp && ldg<uint64_t>(p.table + (int64_t)threadIdx.x * 6) != 0;
   ensure_x(p, state);
-  if (e < p.n_exp)
-    router_row(wv, g_tile, p.m, p.d, e, p.n_exp, p.bias, p.logits ? p.logits + e : nullptr, p.scores + e);
+#pragma unroll 1
+  for (int t = 0; t < p.m; ++t) {
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 0; j < kRtChunks; ++j) {
+      const int c = threadIdx.x + kThreads * j;
+      if (c < nch) acc = dot8_f64(reinterpret_cast<const uint4*>(g_tile + t * p.d)[c], wv[j], acc);
+    }
+    acc = wave_sum_f64(acc);
+    if (lane == 0) sh.rpart[wave][t] = acc;
+  }
+  __syncthreads();
+  if (threadIdx.x < p.n_exp) sh.valid[threadIdx.x] = has_entry;
+  if (threadIdx.x < p.m) {
+    const int t = threadIdx.x;
+    double sum = sh.rpart[0][t];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) sum += sh.rpart[w][t];
+    const float score = router_score(sum, p.bias, e, p.logits ? p.logits + t * p.n_exp + e : nullptr);
+    store_agent(p.scores + t * p.n_exp + e, score);
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    sh.flag = add_agent(p.ctl + kCtlRouter, 1u) == (unsigned)(p.n_router - 1);
-    if (sh.flag) set_flag(p.ctl, kFlagRouter);
+    const int g = q / kRouterGroup;
+    const int n_groups = (p.n_router + kRouterGroup - 1) / kRouterGroup;
+    const int in_group = p.n_router - g * kRouterGroup < kRouterGroup ? p.n_router - g * kRouterGroup : kRouterGroup;
+    bool last = add_agent(p.ctl + kCtlRouterGrp + 64 * g, 1u) == (unsigned)(in_group - 1);
+    if (last) last = add_agent(p.ctl + kCtlRouter, 1u) == (unsigned)(n_groups - 1);
+    sh.flag = last;
   }
   __syncthreads();
   return state;
@@ -299,7 +379,7 @@ __device__ __noinline__ int gate_up_item(uint64_t kernarg, int q_arg, int state_
   const int per = (p.d / 128) / kWaves;
   const int st0 = wave * per;
   f32x4 ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
-  gate_up_slot(slot_format(p.scale_fmt, ent, is_shared), ent, g_tile, p.m, p.d, r0, st0, st0 + per, ag, au);
+  gate_up_slot(slot_format(p.scale_fmt, ent, is_shared), ent, g_tile, p.m, p.d, p.i, r0, st0, st0 + per, ag, au);
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int row = 4 * (lane >> 4) + c, col = lane & 15;
@@ -353,7 +433,7 @@ __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg
   unsigned* const ctl = p.ctl;
   const float* const src = p.act + (int64_t)s * m * i;
   f32x4 acc = {0, 0, 0, 0};
-  down_slot(slot_format(p.scale_fmt, ent, is_shared), ent, g_tile, m, i, r0, acc, [&]() __attribute__((always_inline)) {
+  down_slot(slot_format(p.scale_fmt, ent, is_shared), ent, g_tile, m, i, p.d, r0, acc, [&]() __attribute__((always_inline)) {
     if (threadIdx.x == 0) wait_flag(ctl, kFlagSlot + 4 * s);
     __syncthreads();
     // fp32 activations -> bf16 hi rows [t][k] and lo rows [m + t][k]
@@ -422,8 +502,6 @@ __device__ __noinline__ void down_finish(uint64_t kernarg, int q_arg) {
 __global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
   int state = 0;  // 1 while the LDS tile holds x
   if (threadIdx.x == 0) g_sh.have_plan = 0;
-  // which experts the table holds (for the slot plan), read once up front
-  for (int e = threadIdx.x; e < p.n_exp; e += kThreads) g_sh.valid[e] = p.table[(int64_t)e * 6] != 0;
   const uint64_t kernarg = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();  // &p
   const int n_items = p.n_items, q_sgu = p.q_sgu, q_sd = p.q_sd, q_gu = p.q_gu, q_down = p.q_down;
   for (int q = blockIdx.x; q < n_items; q += gridDim.x) {
@@ -463,6 +541,7 @@ __global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
   }
   for (int s = threadIdx.x; s <= p.S; s += kThreads) store_agent(p.ctl + kCtlSlot + 16 * s, 0u);
   for (int g = threadIdx.x; g < p.d / kDownRows; g += kThreads) store_agent(p.ctl + kCtlRowGroup + g, 0u);
+  for (int g = threadIdx.x; g < kMaxExperts / kRouterGroup; g += kThreads) store_agent(p.ctl + kCtlRouterGrp + 64 * g, 0u);
   for (int c = threadIdx.x; c < kFlagCopies * (p.S + 2); c += kThreads) {
     const int copy = c % kFlagCopies, f = c / kFlagCopies;  // f = 0: router, f = 1 + s: slot s
     store_agent(p.ctl + kFlagBase + copy * kFlagStride + (f == 0 ? kFlagRouter : kFlagSlot + 4 * (f - 1)), 0u);
@@ -514,7 +593,7 @@ using namespace hsmoe;
 
 extern "C" size_t hsmoe_moe_layer_workspace_size(int64_t m, int64_t d, int64_t i, int64_t n_experts, int top_k) {
   if (m < 1 || d < 1 || i < 1 || n_experts < 1 || top_k < 1) return 0;
-  return kCtlBytes + scores_bytes(m, n_experts) + act_bytes(m, i, top_k) + part_bytes(m, d, top_k);
+  return kCtlBytes + kPlanBytes + scores_bytes(m, n_experts) + act_bytes(m, i, top_k) + part_bytes(m, d, top_k);
 }
 
 extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
@@ -538,6 +617,8 @@ extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64
   if (d % 512 != 0 || i % 512 != 0 || d <= 0 || i <= 0 || d > 8192 || d / kDownRows > kMaxRowGroups)
     return fail(HSMOE_ERR_SHAPE, "%s: d and i must be positive multiples of 512, d <= 8192 (d=%lld i=%lld)", name,
                 (long long)d, (long long)i);
+  if (!expert_fits(d, i))
+    return fail(HSMOE_ERR_SHAPE, "%s: d*i too large (an expert matrix must stay below 4 GiB)", name);
   if (!aligned(x, 16) || !aligned(gate_w, 16)) return fail(HSMOE_ERR_SHAPE, "%s: x and gate_w must be 16-byte aligned", name);
   const size_t need = hsmoe_moe_layer_workspace_size(m, d, i, n_experts, top_k);
   if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
@@ -568,13 +649,15 @@ extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64
   char* ws = (char*)workspace;
   p.ctl = (unsigned*)ws;
   ws += kCtlBytes;
+  p.plan = (unsigned*)ws;
+  ws += kPlanBytes;
   p.scores = (float*)ws;
   ws += scores_bytes(m, n_experts);
   p.act = (float*)ws;
   ws += act_bytes(m, i, top_k);
   p.part = (float*)ws;
   const int has_shared = shared ? 1 : 0;
-  p.n_router = (int)((n_experts + kWaves - 1) / kWaves);
+  p.n_router = (int)n_experts;
   p.q_sgu = p.n_router;
   p.q_sd = p.q_sgu + has_shared * (int)(i / kGuRows);
   p.q_gu = p.q_sd + has_shared * (int)(d / kDownRows);

@@ -244,24 +244,27 @@ template <int F, int kMats, int kRT>
 struct WBuf {
   static constexpr int kSteps = kCols / 128;
   Batch<F, kSteps> b[kMats][kRT];
-  __device__ __forceinline__ void load(const uint64_t* ent, int w_slot, int64_t row, int64_t k, int kc, int g) {
+  __device__ __forceinline__ void load(const Mat (&mats)[kMats], int row, int k, int kc, int g) {
 #pragma unroll
     for (int q = 0; q < kMats; ++q)
 #pragma unroll
-      for (int rt = 0; rt < kRT; ++rt)
-        b[q][rt].load(ent[w_slot + 2 * q], ent[w_slot + 2 * q + 1], row + 16 * rt, k, kc * kSteps, g);
+      for (int rt = 0; rt < kRT; ++rt) b[q][rt].load(mats[q], row + 16 * rt, k, kc * kSteps, g);
   }
 };
 
-// Software pipeline over K-chunks.  While chunk kc is multiplied, the token
+// Software pipeline over K-chunks of the kMats matrices ([n_rows][k]) at
+// ent[w_slot], ent[w_slot + 2], ...  While chunk kc is multiplied, the token
 // tile of kc + 1 is in flight to registers and the weights of kc + 2 to the
 // third weight buffer; the tile loads are issued before the weight loads.
 // Buffers rotate statically (three steps per loop turn).
 template <int F, int kMats, int kRT, int kPlanes, typename Src, typename Mul>
-__device__ __forceinline__ void pipeline(const uint64_t* ent, int w_slot, int64_t row, int64_t k, int g, int n,
+__device__ __forceinline__ void pipeline(const uint64_t* ent, int w_slot, int n_rows, int row, int k, int g, int n,
                                          uint16_t* lds, Src&& src, Mul&& mul) {
   using W = WBuf<F, kMats, kRT>;
-  const int nkc = (int)(k / kCols);
+  const int nkc = k / kCols;
+  Mat mats[kMats];
+#pragma unroll
+  for (int q = 0; q < kMats; ++q) mats[q] = make_mat<F>(ent[w_slot + 2 * q], ent[w_slot + 2 * q + 1], n_rows, k);
   XStage<kPlanes> xr;
   if constexpr (F == kBf16) {
     // bf16 weights (a compatibility format, 4x the bytes): one buffer, no
@@ -269,7 +272,7 @@ __device__ __forceinline__ void pipeline(const uint64_t* ent, int w_slot, int64_
     W w;
     for (int kc = 0; kc < nkc; ++kc) {
       xr.load(src, kc, n);
-      w.load(ent, w_slot, row, k, kc, g);
+      w.load(mats, row, k, kc, g);
       __syncthreads();
       xr.store(lds);
       __syncthreads();
@@ -279,14 +282,14 @@ __device__ __forceinline__ void pipeline(const uint64_t* ent, int w_slot, int64_
   }
   W w0, w1, w2;
   xr.load(src, 0, n);
-  w0.load(ent, w_slot, row, k, 0, g);
-  if (nkc > 1) w1.load(ent, w_slot, row, k, 1, g);
+  w0.load(mats, row, k, 0, g);
+  if (nkc > 1) w1.load(mats, row, k, 1, g);
   auto step = [&](const W& wc, W& wl, int kc) {
     __syncthreads();
     xr.store(lds);
     __syncthreads();
     if (kc + 1 < nkc) xr.load(src, kc + 1, n);
-    if (kc + 2 < nkc) wl.load(ent, w_slot, row, k, kc + 2, g);
+    if (kc + 2 < nkc) wl.load(mats, row, k, kc + 2, g);
     mul(wc);
   };
   for (int kc = 0; kc < nkc; kc += 3) {
@@ -310,7 +313,7 @@ __device__ void gate_up_chunk(const PrefillParams& p, const Chunk& ch, int r0, u
 #pragma unroll
     for (int t = 0; t < 2; ++t) ag[rt][t] = au[rt][t] = f32x4{0, 0, 0, 0};
   auto src = [&](int, int tt) { return p.x + (int64_t)s_tok[tt] * p.d; };
-  pipeline<F, 2, kGuRT, 1>(ch.ent, 0, r0 + r, p.d, g, ch.n, xs, src, [&](const W& w) {
+  pipeline<F, 2, kGuRT, 1>(ch.ent, 0, p.i, r0 + r, p.d, g, ch.n, xs, src, [&](const W& w) {
 #pragma unroll
     for (int b = 0; b < W::kSteps; ++b) {
 #pragma unroll
@@ -378,7 +381,7 @@ __device__ void down_chunk(const PrefillParams& p, const Chunk& ch, int r0, uint
 #pragma unroll
   for (int rt = 0; rt < kDnRT; ++rt) acc[rt][0] = acc[rt][1] = f32x4{0, 0, 0, 0};
   auto src = [&](int pl, int tt) { return (pl ? p.act_lo : p.act_hi) + (int64_t)(ch.p0 + tt) * p.i; };
-  pipeline<F, 1, kDnRT, 2>(ch.ent, 4, r0 + r, p.i, g, ch.n, as, src, [&](const W& w) {
+  pipeline<F, 1, kDnRT, 2>(ch.ent, 4, p.d, r0 + r, p.i, g, ch.n, as, src, [&](const W& w) {
 #pragma unroll
     for (int b = 0; b < W::kSteps; ++b) {
 #pragma unroll
@@ -516,6 +519,8 @@ extern "C" int hsmoe_moe_prefill(const void* x, int64_t m, int64_t d, int64_t i,
   if (d % 1024 != 0 || i % 512 != 0 || d > 65536 || i > 65536)
     return fail(HSMOE_ERR_SHAPE, "%s: d must be a multiple of 1024 and i of 512 (d=%lld i=%lld)", name, (long long)d,
                 (long long)i);
+  if (!expert_fits(d, i))
+    return fail(HSMOE_ERR_SHAPE, "%s: d*i too large (an expert matrix must stay below 4 GiB)", name);
   if (!aligned(x, 16) || (out_f32 && !aligned(out_f32, 16)) || (out_bf16 && !aligned(out_bf16, 8)))
     return fail(HSMOE_ERR_SHAPE, "%s: x and out_f32 must be 16-byte aligned, out_bf16 8-byte aligned", name);
   const Layout L = layout(m, d, i, n_experts, top_k);

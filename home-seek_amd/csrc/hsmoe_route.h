@@ -137,12 +137,32 @@ __device__ __forceinline__ void load_gate_row(const uint16_t* w, int64_t e, int6
     if (lane * 8 + 512 * c < d) wv[c] = *reinterpret_cast<const uint4*>(wr + lane * 8 + 512 * c);
 }
 
+// The score of expert e from its exact logit sum (fp64): logit =
+// bf16(sum), then bf16(logit + bf16(bias[e])) with a bias; the bf16 logit goes
+// to *logit_out when non-null; score = sqrt(softplus(float(logit))).
+__device__ __forceinline__ float router_score(double sum, const float* bias, int64_t e, uint16_t* logit_out) {
+  uint32_t l = f64_to_bf16_bits(sum);
+  if (bias) l = f32_to_bf16_bits(__fadd_rn(bf16_bits_to_f32(l), bf16_bits_to_f32(f32_to_bf16_bits(bias[e]))));
+  if (logit_out) *logit_out = (uint16_t)l;
+  return sqrtf(softplus_f32(bf16_bits_to_f32(l)));
+}
+
+// Exact products of 8 bf16 pairs (a packed uint4 each) added to acc in fp64,
+// element order.
+__device__ __forceinline__ double dot8_f64(uint4 xv, uint4 wv, double acc) {
+  const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    acc = __fma_rn((double)__uint_as_float(xx[q] << 16), (double)__uint_as_float(ww[q] << 16), acc);
+    acc = __fma_rn((double)__uint_as_float(xx[q] & 0xffff0000u), (double)__uint_as_float(ww[q] & 0xffff0000u), acc);
+  }
+  return acc;
+}
+
 __device__ __forceinline__ void router_row(const uint4 (&wv)[kMaxChunks], const uint16_t* xs, int nt, int64_t d,
                                            int64_t e, int64_t n_exp, const float* bias, uint16_t* logits_row,
                                            float* scores) {
   const int lane = threadIdx.x & 63;
-  float b = 0.0f;
-  if (bias) b = bf16_bits_to_f32(f32_to_bf16_bits(bias[e]));
   // One token at a time (a rolled loop: the unrolled token loop made this the
   // largest straight-line code of the layer kernel, fetched cold by every
   // router item); per token the sum runs over chunks, then words, in order.
@@ -168,10 +188,7 @@ __device__ __forceinline__ void router_row(const uint4 (&wv)[kMaxChunks], const 
     }
     const double sum = wave_sum_f64(acc);
     if (lane == 0) {
-      uint32_t l = f64_to_bf16_bits(sum);
-      if (bias) l = f32_to_bf16_bits(__fadd_rn(bf16_bits_to_f32(l), b));
-      if (logits_row) logits_row[t * n_exp] = (uint16_t)l;
-      const float score = sqrtf(softplus_f32(bf16_bits_to_f32(l)));
+      const float score = router_score(sum, bias, e, logits_row ? logits_row + t * n_exp : nullptr);
       __hip_atomic_store(scores + t * n_exp, score, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }

@@ -18,6 +18,33 @@ namespace hsmoe {
 
 enum Fmt : int { kFp4E8M0 = 0, kFp4F32 = 1, kFp8Block = 2, kBf16 = 3 };
 
+// One weight matrix of format F ([rows][cols], row-major) and its scales, as
+// buffer resources of their exact sizes: every load of a batch is an
+// immediate offset from one per-lane offset, and nothing past either array is
+// read.  Sizes must stay below 4 GiB (the entry points check their shapes).
+struct Mat {
+  BufRsrc w, s;
+};
+template <int F>
+__device__ __forceinline__ Mat make_mat(uint64_t w, uint64_t sc, int rows, int cols) {
+  const uint32_t n = (uint32_t)rows * (uint32_t)cols;
+  Mat m;
+  if constexpr (F == kFp4E8M0) {
+    m.w = make_buf(w, n / 2);
+    m.s = make_buf(sc, n / 32);
+  } else if constexpr (F == kFp4F32) {
+    m.w = make_buf(w, n / 2);
+    m.s = make_buf(sc, n / 32 * 4);
+  } else if constexpr (F == kFp8Block) {
+    m.w = make_buf(w, n);
+    m.s = make_buf(sc, (uint32_t)((rows + 127) / 128) * (uint32_t)((cols + 127) / 128) * 4);
+  } else {
+    m.w = make_buf(w, 2 * n);
+    m.s = make_buf(w, 0);
+  }
+  return m;
+}
+
 template <int F, int kB>
 struct Batch;
 
@@ -26,17 +53,17 @@ struct Batch<kFp4E8M0, kB> {
   uint4 a[kB];
   uint4 sq[kB >= 4 ? kB / 4 : 1];  // kB >= 4: 16 scale bytes per 4 steps (bytes 4b..4b+3 = step b)
   uint32_t sb[kB];                 // kB < 4: one scale byte per step
-  __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
-    const uint8_t* base = (const uint8_t*)w + row * (k / 2) + st * 64 + g * 16;
+  __device__ __forceinline__ void load(const Mat& m, int row, int k, int st, int g) {
+    const uint32_t wo = (uint32_t)row * (uint32_t)(k / 2) + st * 64 + g * 16;
 #pragma unroll
-    for (int b = 0; b < kB; ++b) a[b] = ldg<uint4>(base + b * 64);
-    const uint8_t* sp = (const uint8_t*)sc + row * (k / 32) + st * 4;
+    for (int b = 0; b < kB; ++b) a[b] = bload128(m.w, wo + b * 64);
+    const uint32_t so = (uint32_t)row * (uint32_t)(k / 32) + st * 4;
     if constexpr (kB >= 4) {
 #pragma unroll
-      for (int q = 0; q < kB / 4; ++q) sq[q] = ldg<uint4>(sp + 16 * q);
+      for (int q = 0; q < kB / 4; ++q) sq[q] = bload128(m.s, so + 16 * q);
     } else {
 #pragma unroll
-      for (int b = 0; b < kB; ++b) sb[b] = ldg<uint8_t>(sp + 4 * b + g);
+      for (int b = 0; b < kB; ++b) sb[b] = bload8(m.s, so + 4 * b + g);
     }
   }
   __device__ __forceinline__ bf16x8 frag(int b, int j, int g) const {
@@ -59,13 +86,13 @@ template <int kB>
 struct Batch<kFp4F32, kB> {
   uint4 a[kB];
   float s[kB];
-  __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
-    const uint8_t* base = (const uint8_t*)w + row * (k / 2) + st * 64 + g * 16;
-    const float* sp = (const float*)sc + row * (k / 32) + st * 4 + g;
+  __device__ __forceinline__ void load(const Mat& m, int row, int k, int st, int g) {
+    const uint32_t wo = (uint32_t)row * (uint32_t)(k / 2) + st * 64 + g * 16;
+    const uint32_t so = 4 * ((uint32_t)row * (uint32_t)(k / 32) + st * 4 + g);
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
-      a[b] = ldg<uint4>(base + b * 64);
-      s[b] = ldg<float>(sp + 4 * b);
+      a[b] = bload128(m.w, wo + b * 64);
+      s[b] = bloadf(m.s, so + 16 * b);
     }
   }
   __device__ __forceinline__ bf16x8 frag(int b, int j, int) const {
@@ -79,14 +106,14 @@ template <int kB>
 struct Batch<kFp8Block, kB> {
   uint4 a[kB], c[kB];
   float s[kB];
-  __device__ __forceinline__ void load(uint64_t w, uint64_t sc, int64_t row, int64_t k, int64_t st, int g) {
-    const uint8_t* base = (const uint8_t*)w + row * k + st * 128 + g * 32;
-    const float* sp = (const float*)sc + (row / 128) * (k / 128) + st;
+  __device__ __forceinline__ void load(const Mat& m, int row, int k, int st, int g) {
+    const uint32_t wo = (uint32_t)row * (uint32_t)k + st * 128 + g * 32;
+    const uint32_t so = 4 * ((uint32_t)(row / 128) * (uint32_t)(k / 128) + st);
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
-      a[b] = ldg<uint4>(base + b * 128);
-      c[b] = ldg<uint4>(base + b * 128 + 16);
-      s[b] = ldg<float>(sp + b);
+      a[b] = bload128(m.w, wo + b * 128);
+      c[b] = bload128(m.w, wo + b * 128 + 16);
+      s[b] = bloadf(m.s, so + 4 * b);
     }
   }
   __device__ __forceinline__ bf16x8 frag(int b, int j, int) const {
@@ -102,12 +129,12 @@ struct Batch<kFp8Block, kB> {
 template <int kB>
 struct Batch<kBf16, kB> {
   uint4 a[kB][4];
-  __device__ __forceinline__ void load(uint64_t w, uint64_t, int64_t row, int64_t k, int64_t st, int g) {
-    const uint4* base = reinterpret_cast<const uint4*>((const uint16_t*)w + row * k + st * 128 + g * 32);
+  __device__ __forceinline__ void load(const Mat& m, int row, int k, int st, int g) {
+    const uint32_t wo = 2 * ((uint32_t)row * (uint32_t)k + st * 128 + g * 32);
 #pragma unroll
     for (int b = 0; b < kB; ++b)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) a[b][j] = ldg<uint4>(base + b * 16 + j);
+      for (int j = 0; j < 4; ++j) a[b][j] = bload128(m.w, wo + b * 256 + j * 16);
   }
   __device__ __forceinline__ bf16x8 frag(int b, int j, int) const { return __builtin_bit_cast(bf16x8, a[b][j]); }
 };
@@ -146,19 +173,20 @@ __device__ __forceinline__ bf16x8 lds_frag(const uint16_t* tile, int kcols, int 
 }
 
 // ------------------------------------------------------------ gate / up
-// One wave: rows r0..r0+15 of W1 and W3 of the slot `ent` over steps
+// One wave: rows r0..r0+15 of W1 and W3 ([i][d]) of the slot `ent` over steps
 // [st0, st1) against the m token rows of x ([m][d] bf16 in LDS).  The MFMA
 // accumulators hold D[4*(lane/16) + q][lane%16] = row r0 + 4*(lane/16) + q,
 // token lane%16.
 template <int F, int kB>
-__device__ __forceinline__ void gate_up_rows(const uint64_t* ent, const uint16_t* xs, int m, int d, int r0, int st0,
-                                             int st1, f32x4& ag, f32x4& au) {
+__device__ __forceinline__ void gate_up_rows(const uint64_t* ent, const uint16_t* xs, int m, int d, int i, int r0,
+                                             int st0, int st1, f32x4& ag, f32x4& au) {
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  const int64_t row = r0 + r;
+  const int row = r0 + r;
+  const Mat w1 = make_mat<F>(ent[0], ent[1], i, d), w3 = make_mat<F>(ent[2], ent[3], i, d);
   for (int st = st0; st < st1; st += kB) {
     Batch<F, kB> b1, b3;
-    b1.load(ent[0], ent[1], row, d, st, g);
-    b3.load(ent[2], ent[3], row, d, st, g);
+    b1.load(w1, row, d, st, g);
+    b3.load(w3, row, d, st, g);
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
 #pragma unroll
@@ -172,23 +200,23 @@ __device__ __forceinline__ void gate_up_rows(const uint64_t* ent, const uint16_t
 }
 
 template <int F>
-__device__ __forceinline__ void gate_up_any(const uint64_t* ent, const uint16_t* xs, int m, int d, int r0, int st0,
-                                            int st1, f32x4& ag, f32x4& au) {
+__device__ __forceinline__ void gate_up_any(const uint64_t* ent, const uint16_t* xs, int m, int d, int i, int r0,
+                                            int st0, int st1, f32x4& ag, f32x4& au) {
   constexpr int kMax = gate_up_batch<F>();
   const int b = batch_for<kMax>(st1 - st0);
-  if (b == kMax) gate_up_rows<F, kMax>(ent, xs, m, d, r0, st0, st1, ag, au);
-  else if (kMax > 4 && b == 4) gate_up_rows<F, (kMax > 4 ? 4 : 1)>(ent, xs, m, d, r0, st0, st1, ag, au);
-  else if (kMax > 2 && b == 2) gate_up_rows<F, (kMax > 2 ? 2 : 1)>(ent, xs, m, d, r0, st0, st1, ag, au);
-  else gate_up_rows<F, 1>(ent, xs, m, d, r0, st0, st1, ag, au);
+  if (b == kMax) gate_up_rows<F, kMax>(ent, xs, m, d, i, r0, st0, st1, ag, au);
+  else if (kMax > 4 && b == 4) gate_up_rows<F, (kMax > 4 ? 4 : 1)>(ent, xs, m, d, i, r0, st0, st1, ag, au);
+  else if (kMax > 2 && b == 2) gate_up_rows<F, (kMax > 2 ? 2 : 1)>(ent, xs, m, d, i, r0, st0, st1, ag, au);
+  else gate_up_rows<F, 1>(ent, xs, m, d, i, r0, st0, st1, ag, au);
 }
 
-__device__ __forceinline__ void gate_up_slot(int fmt, const uint64_t* ent, const uint16_t* xs, int m, int d, int r0,
-                                             int st0, int st1, f32x4& ag, f32x4& au) {
+__device__ __forceinline__ void gate_up_slot(int fmt, const uint64_t* ent, const uint16_t* xs, int m, int d, int i,
+                                             int r0, int st0, int st1, f32x4& ag, f32x4& au) {
   switch (fmt) {
-    case kFp4E8M0: gate_up_any<kFp4E8M0>(ent, xs, m, d, r0, st0, st1, ag, au); break;
-    case kFp4F32: gate_up_any<kFp4F32>(ent, xs, m, d, r0, st0, st1, ag, au); break;
-    case kFp8Block: gate_up_any<kFp8Block>(ent, xs, m, d, r0, st0, st1, ag, au); break;
-    default: gate_up_any<kBf16>(ent, xs, m, d, r0, st0, st1, ag, au); break;
+    case kFp4E8M0: gate_up_any<kFp4E8M0>(ent, xs, m, d, i, r0, st0, st1, ag, au); break;
+    case kFp4F32: gate_up_any<kFp4F32>(ent, xs, m, d, i, r0, st0, st1, ag, au); break;
+    case kFp8Block: gate_up_any<kFp8Block>(ent, xs, m, d, i, r0, st0, st1, ag, au); break;
+    default: gate_up_any<kBf16>(ent, xs, m, d, i, r0, st0, st1, ag, au); break;
   }
 }
 
@@ -202,21 +230,23 @@ __device__ __forceinline__ float swiglu(float gsum, float usum, float L) {
 }
 
 // ------------------------------------------------------------ down
-// One wave: rows r0..r0+15 of W2 of the slot `ent` over all i/128 steps
-// against the activation tile as ([2m][i] bf16 in LDS: hi rows then lo rows).
-// `ready()` runs (block-wide) after the first batch's loads are issued and
-// before the tile is read, so the weight loads overlap whatever it waits for.
+// One wave: rows r0..r0+15 of W2 ([d][i]) of the slot `ent` over all i/128
+// steps against the activation tile as ([2m][i] bf16 in LDS: hi rows then lo
+// rows).  `ready()` runs (block-wide) after the first batch's loads are issued
+// and before the tile is read, so the weight loads overlap whatever it waits
+// for.
 template <int F, int kB, typename Ready>
-__device__ __forceinline__ void down_rows(const uint64_t* ent, const uint16_t* as, int m, int i, int r0, f32x4& acc,
-                                          Ready&& ready) {
+__device__ __forceinline__ void down_rows(const uint64_t* ent, const uint16_t* as, int m, int i, int d, int r0,
+                                          f32x4& acc, Ready&& ready) {
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  const int64_t row = r0 + r;
+  const int row = r0 + r;
   const int n = i / 128;
+  const Mat w2 = make_mat<F>(ent[4], ent[5], d, i);
   Batch<F, kB> bw;
-  bw.load(ent[4], ent[5], row, i, 0, g);
+  bw.load(w2, row, i, 0, g);
   ready();
   for (int st = 0; st < n; st += kB) {
-    if (st) bw.load(ent[4], ent[5], row, i, st, g);
+    if (st) bw.load(w2, row, i, st, g);
 #pragma unroll
     for (int b = 0; b < kB; ++b)
 #pragma unroll
@@ -225,25 +255,25 @@ __device__ __forceinline__ void down_rows(const uint64_t* ent, const uint16_t* a
 }
 
 template <int F, typename Ready>
-__device__ __forceinline__ void down_any(const uint64_t* ent, const uint16_t* as, int m, int i, int r0, f32x4& acc,
-                                         Ready&& ready) {
+__device__ __forceinline__ void down_any(const uint64_t* ent, const uint16_t* as, int m, int i, int d, int r0,
+                                         f32x4& acc, Ready&& ready) {
   constexpr int kMax = down_batch<F>();
   const int b = batch_for<kMax>(i / 128);
-  if (b == kMax) down_rows<F, kMax>(ent, as, m, i, r0, acc, ready);
-  else if (kMax > 8 && b == 8) down_rows<F, (kMax > 8 ? 8 : 1)>(ent, as, m, i, r0, acc, ready);
-  else if (kMax > 4 && b == 4) down_rows<F, (kMax > 4 ? 4 : 1)>(ent, as, m, i, r0, acc, ready);
-  else if (kMax > 2 && b == 2) down_rows<F, (kMax > 2 ? 2 : 1)>(ent, as, m, i, r0, acc, ready);
-  else down_rows<F, 1>(ent, as, m, i, r0, acc, ready);
+  if (b == kMax) down_rows<F, kMax>(ent, as, m, i, d, r0, acc, ready);
+  else if (kMax > 8 && b == 8) down_rows<F, (kMax > 8 ? 8 : 1)>(ent, as, m, i, d, r0, acc, ready);
+  else if (kMax > 4 && b == 4) down_rows<F, (kMax > 4 ? 4 : 1)>(ent, as, m, i, d, r0, acc, ready);
+  else if (kMax > 2 && b == 2) down_rows<F, (kMax > 2 ? 2 : 1)>(ent, as, m, i, d, r0, acc, ready);
+  else down_rows<F, 1>(ent, as, m, i, d, r0, acc, ready);
 }
 
 template <typename Ready>
-__device__ __forceinline__ void down_slot(int fmt, const uint64_t* ent, const uint16_t* as, int m, int i, int r0,
-                                          f32x4& acc, Ready&& ready) {
+__device__ __forceinline__ void down_slot(int fmt, const uint64_t* ent, const uint16_t* as, int m, int i, int d,
+                                          int r0, f32x4& acc, Ready&& ready) {
   switch (fmt) {
-    case kFp4E8M0: down_any<kFp4E8M0>(ent, as, m, i, r0, acc, ready); break;
-    case kFp4F32: down_any<kFp4F32>(ent, as, m, i, r0, acc, ready); break;
-    case kFp8Block: down_any<kFp8Block>(ent, as, m, i, r0, acc, ready); break;
-    default: down_any<kBf16>(ent, as, m, i, r0, acc, ready); break;
+    case kFp4E8M0: down_any<kFp4E8M0>(ent, as, m, i, d, r0, acc, ready); break;
+    case kFp4F32: down_any<kFp4F32>(ent, as, m, i, d, r0, acc, ready); break;
+    case kFp8Block: down_any<kFp8Block>(ent, as, m, i, d, r0, acc, ready); break;
+    default: down_any<kBf16>(ent, as, m, i, d, r0, acc, ready); break;
   }
 }
 
