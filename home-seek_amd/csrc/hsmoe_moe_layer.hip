@@ -75,16 +75,17 @@ constexpr int kRouterGroup = 16;     // router items per group counter (at most 
 constexpr int kFlagCopies = 8;
 constexpr int kFlagBase = 8192;      // word index of flag copy 0 (32 KiB)
 constexpr int kFlagStride = 1024;    // words between copies (4 KiB)
-constexpr int kFlagRouter = 0;       // + copy: every router item finished
+constexpr int kFlagRouter = 0;       // + copy: the slot plan is published
 constexpr int kFlagSlot = 16;        // + 4*s: every gate/up item of slot s finished
 constexpr size_t kCtlBytes = 65536;
 static_assert(kCtlRowGroup + kMaxRowGroups <= kCtlRouterGrp, "control block overflow");
 static_assert(kCtlRouterGrp + 64 * (kMaxExperts / kRouterGroup) <= kFlagBase, "control block overflow");
 // Published plan, one copy per flag copy: [0] slot count, [1 + s] expert id of
-// slot s, [1 + S + s*m + t] weight of slot s for token t (S = m * top_k).
-constexpr int kPlanStride = 2048;  // words between copies (8 KiB)
+// slot s, [1 + S + s*m + t] weight of slot s for token t, [1 + S + S*m + 12s]
+// the slot's table entry (6 pointers as 12 words) (S = m * top_k).
+constexpr int kPlanStride = 4096;  // words between copies (16 KiB)
 constexpr size_t kPlanBytes = (size_t)kFlagCopies * kPlanStride * 4;
-static_assert(1 + kMaxSlots + kMaxSlots * kMaxTok <= kPlanStride, "plan copy overflow");
+static_assert(1 + kMaxSlots + kMaxSlots * kMaxTok + 12 * kMaxSlots <= kPlanStride, "plan copy overflow");
 static_assert(kFlagSlot + 4 * (kMaxSlots + 1) <= kFlagStride, "flag block overflow");
 static_assert((kFlagBase + kFlagCopies * kFlagStride) * 4 <= (int)kCtlBytes, "flag copies overflow");
 
@@ -134,7 +135,8 @@ __device__ __forceinline__ void set_flag(unsigned* ctl, int flag) {
 }
 
 struct Shared {
-  float red[kWaves][2][256];
+  uint64_t ent[kMaxSlots + 1][6];     // table entry of routed slot s (and of the shared expert at slot S)
+  float red[kWaves][2][16 * kMaxTok];  // gate/up partials: [wave][gate|up][row * kMaxTok + token]
   double rpart[kWaves][kMaxTok];  // router: per-wave partial logit sums
   int64_t idx[kMaxSlots];  // top-k ids of every token
   float w[kMaxSlots];      // top-k weights of every token
@@ -158,6 +160,12 @@ struct Shared {
 __device__ __forceinline__ void build_plan(const LayerParams& p, Shared& sh) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = p.m * p.top_k;
+  // thread e holds expert e's table entry, loaded alongside the scores; the
+  // selected ones go to sh.ent below (n_exp <= kThreads)
+  uint64_t my_ent[6];
+#pragma unroll
+  for (int k = 0; k < 6; ++k)
+    my_ent[k] = (int)threadIdx.x < p.n_exp ? ldg<uint64_t>(p.table + (int64_t)threadIdx.x * 6 + k) : 0ull;
   // (sh.valid was filled by this workgroup's router item)
   for (int e = threadIdx.x; e < p.n_exp; e += kThreads) sh.used[e] = 0;
   __syncthreads();
@@ -188,6 +196,10 @@ __device__ __forceinline__ void build_plan(const LayerParams& p, Shared& sh) {
     if (u) {
       sh.rank[e] = (short)(off + below);
       sh.eid[off + below] = e;
+      if (e0 == 0) {  // e == threadIdx.x: this thread holds the entry
+#pragma unroll
+        for (int k = 0; k < 6; ++k) sh.ent[off + below][k] = my_ent[k];
+      }
     }
     for (int w = 0; w < kWaves; ++w) base += sh.wave_count[w];
     __syncthreads();
@@ -255,14 +267,18 @@ __device__ __forceinline__ LayerParams params(uint64_t kernarg) {
 __device__ __noinline__ void plan_item(uint64_t kernarg, int publish) {
   const LayerParams p = params(kernarg);
   Shared& sh = g_sh;
-  const int S = p.S, m = p.m, words = 1 + S + S * m;
+  const int S = p.S, m = p.m, e0 = 1 + S + S * m, words = e0 + 12 * S;
   if (__builtin_amdgcn_readfirstlane(publish)) {
     build_plan(p, sh);
     for (int k = threadIdx.x; k < words; k += kThreads) {
       unsigned v;
       if (k == 0) v = (unsigned)sh.n_routed;
       else if (k <= S) v = (unsigned)sh.eid[k - 1];
-      else v = __float_as_uint(sh.wt[(k - 1 - S) / m][(k - 1 - S) % m]);
+      else if (k < e0) v = __float_as_uint(sh.wt[(k - 1 - S) / m][(k - 1 - S) % m]);
+      else {
+        const uint64_t ev = sh.ent[(k - e0) / 12][((k - e0) % 12) / 2];
+        v = (k - e0) % 2 ? (unsigned)(ev >> 32) : (unsigned)ev;
+      }
 #pragma unroll
       for (int c = 0; c < kFlagCopies; ++c) store_agent(p.plan + c * kPlanStride + k, v);
     }
@@ -279,7 +295,8 @@ __device__ __noinline__ void plan_item(uint64_t kernarg, int publish) {
     const unsigned v = load_agent(src + k);
     if (k == 0) sh.n_routed = (int)v;
     else if (k <= S) sh.eid[k - 1] = (int)v;
-    else sh.wt[(k - 1 - S) / m][(k - 1 - S) % m] = __uint_as_float(v);
+    else if (k < e0) sh.wt[(k - 1 - S) / m][(k - 1 - S) % m] = __uint_as_float(v);
+    else reinterpret_cast<unsigned*>(sh.ent[(k - e0) / 12])[(k - e0) % 12] = v;
   }
   if (threadIdx.x == 0) sh.have_plan = 1;
   __syncthreads();
@@ -374,17 +391,19 @@ __device__ __noinline__ int gate_up_item(uint64_t kernarg, int q_arg, int state_
   const int r0 = (qq % gu_per_slot) * kGuRows;
   if (!is_shared && s >= sh.n_routed) return state;
   if (threadIdx.x < p.m) sh.wt_item[threadIdx.x] = is_shared ? 1.0f : sh.wt[s][threadIdx.x];
-  const uint64_t* ent = is_shared ? p.shared : p.table + (int64_t)sh.eid[s] * 6;
+  const uint64_t* ent = sh.ent[s];
   ensure_x(p, state);
   const int per = (p.d / 128) / kWaves;
   const int st0 = wave * per;
   f32x4 ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
   gate_up_slot(slot_format(p.scale_fmt, ent, is_shared), ent, g_tile, p.m, p.d, p.i, r0, st0, st0 + per, ag, au);
+  if ((lane & 15) < kMaxTok) {
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int row = 4 * (lane >> 4) + c, col = lane & 15;
-    sh.red[wave][0][row * 16 + col] = ag[c];
-    sh.red[wave][1][row * 16 + col] = au[c];
+    for (int c = 0; c < 4; ++c) {
+      const int row = 4 * (lane >> 4) + c, col = lane & 15;
+      sh.red[wave][0][row * kMaxTok + col] = ag[c];
+      sh.red[wave][1][row * kMaxTok + col] = au[c];
+    }
   }
   __syncthreads();
   const int row = threadIdx.x >> 4, col = threadIdx.x & 15;
@@ -392,8 +411,8 @@ __device__ __noinline__ int gate_up_item(uint64_t kernarg, int q_arg, int state_
     float gsum = 0.0f, usum = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      gsum = __fadd_rn(gsum, sh.red[w][0][threadIdx.x]);
-      usum = __fadd_rn(usum, sh.red[w][1][threadIdx.x]);
+      gsum = __fadd_rn(gsum, sh.red[w][0][row * kMaxTok + col]);
+      usum = __fadd_rn(usum, sh.red[w][1][row * kMaxTok + col]);
     }
     const float a = __fmul_rn(sh.wt_item[col], swiglu(gsum, usum, p.limit));
     store_agent(p.act + ((int64_t)s * p.m + col) * p.i + r0 + row, a);
@@ -403,6 +422,101 @@ __device__ __noinline__ int gate_up_item(uint64_t kernarg, int q_arg, int state_
   if (threadIdx.x == 0 && add_agent(p.ctl + kCtlSlot + 16 * s, 1u) == (unsigned)(gu_per_slot - 1))
     set_flag(p.ctl, kFlagSlot + 4 * s);
   return state;
+}
+
+// A run of routed gate/up items q, q + G, q + 2G, ... (G = grid) whose slots
+// are in format F with whole batches (d / 512 a multiple of the batch): as
+// soon as a wave has multiplied its last batch of item q it issues the first
+// batch of item q + G into the same registers, so the cross-wave reduction,
+// the publish and the wait for the stores of item q overlap the loads of the
+// next item.  The slot arrival of item q is counted after its stores are
+// complete; its result (is this the slot's last arrival?) is read one item
+// later, when the loads of the next item have returned anyway, and for the
+// run's last item at the end.  Same tiles and accumulation order as
+// gate_up_item, so the results are identical.  Returns the last item run.
+template <int F>
+__device__ __noinline__ int gate_up_run(uint64_t kernarg, int q_arg, int state_arg) {
+  constexpr int kB = gate_up_batch<F>();
+  int q = __builtin_amdgcn_readfirstlane(q_arg);
+  int state = __builtin_amdgcn_readfirstlane(state_arg);
+  const LayerParams p = params(kernarg);
+  Shared& sh = g_sh;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int G = (int)gridDim.x, gu_per_slot = p.i / kGuRows;
+  const int per = (p.d / 128) / kWaves, nb = per / kB, st0 = wave * per;
+  ensure_x(p, state);
+  int s = (q - p.q_gu) / gu_per_slot, r0 = ((q - p.q_gu) % gu_per_slot) * kGuRows;
+  Mat w1 = make_mat<F>(sh.ent[s][0], sh.ent[s][1], p.i, p.d), w3 = make_mat<F>(sh.ent[s][2], sh.ent[s][3], p.i, p.d);
+  Batch<F, kB> b1, b3;
+  b1.load(w1, r0 + r, p.d, st0, g);
+  b3.load(w3, r0 + r, p.d, st0, g);
+  unsigned pend = 0;  // thread 0: counter value before the previous item's arrival
+  int pend_s = -1;
+  for (;;) {
+    if (threadIdx.x < p.m) sh.wt_item[threadIdx.x] = sh.wt[s][threadIdx.x];
+    f32x4 ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
+    for (int bt = 0; bt < nb; ++bt) {
+      const int st = st0 + bt * kB;
+#pragma unroll
+      for (int b = 0; b < kB; ++b)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8 xf = lds_frag(g_tile, p.d, r, g, st + b, j, p.m);
+          ag = mfma16x16x32(b1.frag(b, j, g), xf, ag);
+          au = mfma16x16x32(b3.frag(b, j, g), xf, au);
+        }
+      if (bt + 1 < nb) {
+        b1.load(w1, r0 + r, p.d, st + kB, g);
+        b3.load(w3, r0 + r, p.d, st + kB, g);
+      }
+    }
+    // the next item of this workgroup, if it continues the run
+    const int q2 = q + G;
+    const int s2 = (q2 - p.q_gu) / gu_per_slot, r02 = ((q2 - p.q_gu) % gu_per_slot) * kGuRows;
+    const bool next = q2 < p.q_down && s2 < sh.n_routed && slot_format(p.scale_fmt, sh.ent[s2], false) == F;
+    if (next) {
+      w1 = make_mat<F>(sh.ent[s2][0], sh.ent[s2][1], p.i, p.d);
+      w3 = make_mat<F>(sh.ent[s2][2], sh.ent[s2][3], p.i, p.d);
+      b1.load(w1, r02 + r, p.d, st0, g);
+      b3.load(w3, r02 + r, p.d, st0, g);
+    }
+    // epilogue of item q (as gate_up_item)
+    if ((lane & 15) < kMaxTok) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int row = 4 * g + c, col = lane & 15;
+        sh.red[wave][0][row * kMaxTok + col] = ag[c];
+        sh.red[wave][1][row * kMaxTok + col] = au[c];
+      }
+    }
+    __syncthreads();
+    {
+      const int row = threadIdx.x >> 4, col = threadIdx.x & 15;
+      if (col < p.m) {
+        float gsum = 0.0f, usum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          gsum = __fadd_rn(gsum, sh.red[w][0][row * kMaxTok + col]);
+          usum = __fadd_rn(usum, sh.red[w][1][row * kMaxTok + col]);
+        }
+        const float a = __fmul_rn(sh.wt_item[col], swiglu(gsum, usum, p.limit));
+        store_agent(p.act + ((int64_t)s * p.m + col) * p.i + r0 + row, a);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the stores of item q (and the next item's loads)
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      if (pend_s >= 0 && pend == (unsigned)(gu_per_slot - 1)) set_flag(p.ctl, kFlagSlot + 4 * pend_s);
+      pend = add_agent(p.ctl + kCtlSlot + 16 * s, 1u);
+      pend_s = s;
+    }
+    if (!next) break;
+    q = q2;
+    s = s2;
+    r0 = r02;
+  }
+  if (threadIdx.x == 0 && pend == (unsigned)(gu_per_slot - 1)) set_flag(p.ctl, kFlagSlot + 4 * pend_s);
+  return q;
 }
 
 // Slot and row group of down item q (shared down items first).
@@ -427,7 +541,7 @@ __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg
   int s, g;
   down_slot_of(p, q, is_shared, s, g);
   if (!is_shared && s >= sh.n_routed) return state;
-  const uint64_t* ent = is_shared ? p.shared : p.table + (int64_t)sh.eid[s] * 6;
+  const uint64_t* ent = sh.ent[s];
   const int r0 = g * kDownRows + 16 * wave;
   const int m = p.m, i = p.i;
   unsigned* const ctl = p.ctl;
@@ -502,6 +616,7 @@ __device__ __noinline__ void down_finish(uint64_t kernarg, int q_arg) {
 __global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
   int state = 0;  // 1 while the LDS tile holds x
   if (threadIdx.x == 0) g_sh.have_plan = 0;
+  if (p.shared && threadIdx.x < 6) g_sh.ent[p.S][threadIdx.x] = ldg<uint64_t>(p.shared + threadIdx.x);
   const uint64_t kernarg = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();  // &p
   const int n_items = p.n_items, q_sgu = p.q_sgu, q_sd = p.q_sd, q_gu = p.q_gu, q_down = p.q_down;
   for (int q = blockIdx.x; q < n_items; q += gridDim.x) {
@@ -523,7 +638,18 @@ __global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
     }
     if (!g_sh.have_plan) plan_item(kernarg, 0);  // routed items need the slot plan
     if (q < q_down) {
-      state = gate_up_item(kernarg, q, state);
+      const int s = (q - q_gu) / (p.i / kGuRows);
+      const int fmt = s < g_sh.n_routed ? slot_format(p.scale_fmt, g_sh.ent[s], false) : -1;
+      const bool whole = ((p.d / 128) / kWaves) % gate_up_batch<kFp4E8M0>() == 0;
+      if (fmt == kFp4E8M0 && whole) {
+        q = gate_up_run<kFp4E8M0>(kernarg, q, state);
+        state = 1;
+      } else if (fmt == kFp4F32 && whole) {
+        q = gate_up_run<kFp4F32>(kernarg, q, state);
+        state = 1;
+      } else {
+        state = gate_up_item(kernarg, q, state);
+      }
     } else {
       state = down_item(kernarg, q, state);
       down_finish(kernarg, q);
@@ -543,7 +669,7 @@ __global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
   for (int g = threadIdx.x; g < p.d / kDownRows; g += kThreads) store_agent(p.ctl + kCtlRowGroup + g, 0u);
   for (int g = threadIdx.x; g < kMaxExperts / kRouterGroup; g += kThreads) store_agent(p.ctl + kCtlRouterGrp + 64 * g, 0u);
   for (int c = threadIdx.x; c < kFlagCopies * (p.S + 2); c += kThreads) {
-    const int copy = c % kFlagCopies, f = c / kFlagCopies;  // f = 0: router, f = 1 + s: slot s
+    const int copy = c % kFlagCopies, f = c / kFlagCopies;  // f = 0: plan, f = 1 + s: slot s
     store_agent(p.ctl + kFlagBase + copy * kFlagStride + (f == 0 ? kFlagRouter : kFlagSlot + 4 * (f - 1)), 0u);
   }
 }
