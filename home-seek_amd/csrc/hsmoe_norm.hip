@@ -12,36 +12,13 @@
 // deterministic.
 #include "hsmoe_common.h"
 #include "hsmoe_internal.h"
+#include "hsmoe_norm.h"
 
 namespace hsmoe {
 namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxD = 16384;
-
-__device__ __forceinline__ uint32_t add_bf16(uint32_t a, uint32_t b) {
-  return f32_to_bf16_bits(__fadd_rn(bf16_bits_to_f32(a), bf16_bits_to_f32(b)));
-}
-
-// Elementwise bf16 add of two packed pairs.
-__device__ __forceinline__ uint32_t add_pair(uint32_t a, uint32_t b) {
-  return add_bf16(a & 0xffffu, b & 0xffffu) | (add_bf16(a >> 16, b >> 16) << 16);
-}
-
-__device__ __forceinline__ uint4 add_chunk(uint4 a, uint4 b) {
-  return make_uint4(add_pair(a.x, b.x), add_pair(a.y, b.y), add_pair(a.z, b.z), add_pair(a.w, b.w));
-}
-
-__device__ __forceinline__ float sumsq_pair(uint32_t p, float s) {
-  const float lo = bf16_bits_to_f32(p & 0xffffu), hi = bf16_bits_to_f32(p >> 16);
-  return __fmaf_rn(hi, hi, __fmaf_rn(lo, lo, s));
-}
-
-__device__ __forceinline__ uint32_t scale_pair(uint32_t x, uint32_t w, float inv) {
-  const float lo = __fmul_rn(bf16_bits_to_f32(w & 0xffffu), __fmul_rn(bf16_bits_to_f32(x & 0xffffu), inv));
-  const float hi = __fmul_rn(bf16_bits_to_f32(w >> 16), __fmul_rn(bf16_bits_to_f32(x >> 16), inv));
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
-}
 
 template <bool kAdd, bool kRes>
 __global__ void __launch_bounds__(kThreads)
@@ -55,26 +32,17 @@ __global__ void __launch_bounds__(kThreads)
   float s = 0.0f;
   for (int c = threadIdx.x; c < chunks; c += kThreads) {
     uint4 v = x[base + c];
-    if (kAdd) v = add_chunk(v, add[base + c]);
-    if (kRes) v = add_chunk(v, res[c]);
+    if (kAdd) v = norm_add_chunk(v, add[base + c]);
+    if (kRes) v = norm_add_chunk(v, res[c]);
     if (h_out) h_out[base + c] = v;
     row[c] = v;
-    s = sumsq_pair(v.w, sumsq_pair(v.z, sumsq_pair(v.y, sumsq_pair(v.x, s))));
+    s = norm_sumsq_chunk(v, s);
   }
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) s = __fadd_rn(s, __shfl_xor(s, off, 64));
+  s = norm_wave_sum(s);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
   __syncthreads();
-  float tot = part[0];
-#pragma unroll
-  for (int q = 1; q < kThreads / 64; ++q) tot = __fadd_rn(tot, part[q]);
-  const float var = __fdiv_rn(tot, (float)d);
-  const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, eps)));
-  for (int c = threadIdx.x; c < chunks; c += kThreads) {
-    const uint4 v = row[c], g = w[c];
-    out[base + c] = make_uint4(scale_pair(v.x, g.x, inv), scale_pair(v.y, g.y, inv), scale_pair(v.z, g.z, inv),
-                               scale_pair(v.w, g.w, inv));
-  }
+  const float inv = norm_inv(part, d, eps);
+  for (int c = threadIdx.x; c < chunks; c += kThreads) out[base + c] = norm_scale_chunk(row[c], w[c], inv);
 }
 
 }  // namespace
