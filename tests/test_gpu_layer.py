@@ -28,17 +28,17 @@ def layer(dev):
     return store, gate, bias
 
 
-def staged(x, gate, bias, table, shared):
+def staged(x, gate, bias, table, shared, kind=ops.SCALE_E8M0):
     idx, w = ops.router_topk(x, gate, bias, K, 1.5)
     f32 = torch.empty(x.shape[0], D, dtype=torch.float32, device=x.device)
-    out, _ = ops.moe_decode(x, idx, w, table, ops.SCALE_E8M0, shared, 10.0, out_f32=f32, d=D, i=I)
+    out, _ = ops.moe_decode(x, idx, w, table, kind, shared, 10.0, out_f32=f32, d=D, i=I)
     return out, f32, idx, w
 
 
-def fused(x, gate, bias, table, shared, **kw):
+def fused(x, gate, bias, table, shared, kind=ops.SCALE_E8M0, **kw):
     """(out_bf16, out_f32, idx, w[, logits]) of the fused launch."""
     f32 = torch.empty(x.shape[0], D, dtype=torch.float32, device=x.device)
-    res = ops.moe_layer_decode(x, gate, bias, table, ops.SCALE_E8M0, shared, I, K, 1.5, 10.0,
+    res = ops.moe_layer_decode(x, gate, bias, table, kind, shared, I, K, 1.5, 10.0,
                                out_bf16=torch.empty(x.shape[0], D, dtype=torch.bfloat16, device=x.device),
                                out_f32=f32, **kw)
     return (res[0], f32) + tuple(res[2:])
@@ -101,6 +101,52 @@ def test_fused_layer_absent_experts_no_shared_no_bias(layer, dev):
     torch.cuda.synchronize()
     assert torch.count_nonzero(z[1]) == 0 and torch.count_nonzero(z[0]) == 0
     assert torch.count_nonzero(zs[1]) == 0 and torch.count_nonzero(zs[0]) == 0
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_fused_layer_fp32_scales_and_bf16_experts(layer, dev, m):
+    """A table in the engine's GPU-tier layout (engine.py:1260-1271): FP4 experts
+    with fp32 block scales, some experts as dequantised bf16 weights
+    (_load_bf16_deq) and one absent.  Runs of FP4 slots stop at the bf16 ones, so
+    the fp32-scale run path and the per-slot path both run in one launch."""
+    store, gate, bias = layer
+    x = synthetic.hidden(SEED, 500 + m, m, D, dev)
+    idx, _ = ops.router_topk(x, gate, bias, K, 1.5)
+    ids = sorted(set(idx.cpu().reshape(-1).tolist()))
+    absent = ids[0]
+    as_bf16 = set(ids[1::3])
+    entries = [None] * E
+    for eid in ids[1:]:
+        w1, s1, w3, s3, w2, s2 = store.expert_views(0, eid)
+        if eid in as_bf16:
+            ent = (ops.fp4_dequant_bf16(w1, s1), ops.fp4_dequant_bf16(w3, s3), ops.fp4_dequant_bf16(w2, s2))
+        else:
+            ent = (w1, s1.to(torch.float32), w3, s3.to(torch.float32), w2, s2.to(torch.float32))
+        entries[eid] = ent
+    table = ops.expert_table(entries, dev)
+    a = fused(x, gate, bias, table, store.shared_entry(0), kind=ops.SCALE_F32)
+    b = staged(x, gate, bias, table, store.shared_entry(0), kind=ops.SCALE_F32)
+    torch.cuda.synchronize()
+    assert ops.moe_layer_status(dev) == 0
+    for got, ref, what in zip(a, b, ("bf16", "f32", "idx", "w")):
+        assert torch.equal(got, ref), what
+    experts = {e: orc.gen_fp4_expert(SEED, 0, e, D, I) for e in ids if e != absent}
+    ref = orc.moe_layer_fp32(orc.to_np_bf16(x), a[2].cpu().numpy(), a[3].cpu().numpy(), experts,
+                             orc.gen_shared_expert(SEED, 0, D, I), 10.0)
+    got = a[1].cpu().numpy().astype(np.float64)
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    mx = np.abs(got - ref).max()
+    print(f"[fused layer fp32 scales + bf16, M={m}] rel-L2 {rel:.3e} max-abs {mx:.3e}")
+    assert rel <= 1e-3 and mx <= 2e-2
+    # the fp32-scale FP4 experts alone equal the E8M0 table bit for bit
+    e8 = store.table(0).clone()
+    e8[[absent] + sorted(as_bf16)] = 0
+    c = fused(x, gate, bias, e8, store.shared_entry(0))
+    only_fp4 = [None if (e == absent or e in as_bf16) else entries[e] for e in range(E)]
+    d = fused(x, gate, bias, ops.expert_table(only_fp4, dev), store.shared_entry(0), kind=ops.SCALE_F32)
+    torch.cuda.synchronize()
+    for got, ref, what in zip(d, c, ("bf16", "f32", "idx", "w")):
+        assert torch.equal(got, ref), what
 
 
 def test_fused_layer_graph_replays(layer, dev):
