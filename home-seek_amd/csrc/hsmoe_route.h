@@ -42,6 +42,22 @@ __device__ __forceinline__ uint64_t dpp_max_step(uint64_t k) {
   return o > k ? o : k;
 }
 
+// The same steps for a 32-bit key (one DPP-fed max per step).
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_max_step32(uint32_t k) {
+  const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)k, (int)k, kCtrl, kRowMask, 0xf, false);
+  return o > k ? o : k;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
+  k = dpp_max_step32<0xb1, 0xf>(k);
+  k = dpp_max_step32<0x4e, 0xf>(k);
+  k = dpp_max_step32<0x141, 0xf>(k);
+  k = dpp_max_step32<0x140, 0xf>(k);
+  k = dpp_max_step32<0x142, 0xa>(k);
+  k = dpp_max_step32<0x143, 0xc>(k);
+  return (uint32_t)__builtin_amdgcn_readlane((int)k, 63);
+}
+
 // Wave-wide maximum of a 64-bit key, returned to every lane: quad swaps,
 // half-row and row mirrors, then the row broadcasts of lane 15 and lane 31
 // leave the maximum in lane 63 (six dependent DPP steps instead of six
@@ -59,19 +75,13 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
 }
 
 // Top-k of one token by one wave: lane l keys experts l, l+64, ... (kPer of
-// them, sorted descending once), and each round retires the wave-wide maximum
-// key, popping it from the head of its lane's list.  `sc` holds the token's
-// fp32 scores, written by other workgroups and read with agent-scope loads.
+// them, v[q] = score of expert l + 64q, sorted descending once), and each
+// round retires the wave-wide maximum key, popping it from the head of its
+// lane's list.
 template <int kPer>
-__device__ __forceinline__ void wave_topk_n(const float* sc, int64_t n_exp, int top_k, float scaling,
-                                            int64_t* idx_out, float* w_out) {
+__device__ __forceinline__ void wave_topk_vals(const float (&v)[kPer], int64_t n_exp, int top_k, float scaling,
+                                               int64_t* idx_out, float* w_out) {
   const int lane = threadIdx.x & 63;
-  float v[kPer];  // every load is issued before any is used (one memory round trip)
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    const int e = lane + 64 * q;
-    v[q] = __hip_atomic_load(sc + (e < n_exp ? e : n_exp - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
   uint64_t key[kPer];
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
@@ -89,8 +99,16 @@ __device__ __forceinline__ void wave_topk_n(const float* sc, int64_t n_exp, int 
   float my_v = 0.0f, sum = 0.0f;
   int my_e = 0;
   for (int r = 0; r < top_k; ++r) {
-    const uint64_t best = wave_max_u64(key[0]);
-    const bool mine = key[0] == best;  // keys are unique: one lane
+    // The lane holding the largest key: when a single lane holds the largest
+    // high half (the score), its key is the largest; otherwise (equal scores)
+    // the full 64-bit maximum decides.  Keys are unique, so one lane wins.
+    const uint32_t hi = (uint32_t)(key[0] >> 32);
+    const uint32_t mhi = wave_max_u32(hi);
+    uint64_t top = __ballot(hi == mhi);
+    if (__popcll(top) != 1) top = __ballot(key[0] == wave_max_u64(key[0]));
+    const int win = (int)__builtin_ctzll(top);
+    const uint64_t best = ((uint64_t)mhi << 32) | (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], win);
+    const bool mine = lane == win;
 #pragma unroll
     for (int q = 0; q + 1 < kPer; ++q) key[q] = mine ? key[q + 1] : key[q];
     key[kPer - 1] = mine ? 0ull : key[kPer - 1];
@@ -109,6 +127,21 @@ __device__ __forceinline__ void wave_topk_n(const float* sc, int64_t n_exp, int 
     idx_out[lane] = my_e;
     w_out[lane] = __fmul_rn(__fdiv_rn(my_v, sum), scaling);
   }
+}
+
+// wave_topk_vals over the token's fp32 scores `sc`, written by other
+// workgroups and read with agent-scope loads.
+template <int kPer>
+__device__ __forceinline__ void wave_topk_n(const float* sc, int64_t n_exp, int top_k, float scaling,
+                                            int64_t* idx_out, float* w_out) {
+  const int lane = threadIdx.x & 63;
+  float v[kPer];  // every load is issued before any is used (one memory round trip)
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int e = lane + 64 * q;
+    v[q] = __hip_atomic_load(sc + (e < n_exp ? e : n_exp - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  wave_topk_vals<kPer>(v, n_exp, top_k, scaling, idx_out, w_out);
 }
 
 __device__ __forceinline__ void wave_topk(const float* sc, int64_t n_exp, int top_k, float scaling, int64_t* idx_out,
@@ -140,11 +173,15 @@ __device__ __forceinline__ void load_gate_row(const uint16_t* w, int64_t e, int6
 // The score of expert e from its exact logit sum (fp64): logit =
 // bf16(sum), then bf16(logit + bf16(bias[e])) with a bias; the bf16 logit goes
 // to *logit_out when non-null; score = sqrt(softplus(float(logit))).
-__device__ __forceinline__ float router_score(double sum, const float* bias, int64_t e, uint16_t* logit_out) {
+// (bias_v: bias[e], already loaded; used when has_bias)
+__device__ __forceinline__ float router_score_v(double sum, bool has_bias, float bias_v, uint16_t* logit_out) {
   uint32_t l = f64_to_bf16_bits(sum);
-  if (bias) l = f32_to_bf16_bits(__fadd_rn(bf16_bits_to_f32(l), bf16_bits_to_f32(f32_to_bf16_bits(bias[e]))));
+  if (has_bias) l = f32_to_bf16_bits(__fadd_rn(bf16_bits_to_f32(l), bf16_bits_to_f32(f32_to_bf16_bits(bias_v))));
   if (logit_out) *logit_out = (uint16_t)l;
   return sqrtf(softplus_f32(bf16_bits_to_f32(l)));
+}
+__device__ __forceinline__ float router_score(double sum, const float* bias, int64_t e, uint16_t* logit_out) {
+  return router_score_v(sum, bias != nullptr, bias ? bias[e] : 0.0f, logit_out);
 }
 
 // Exact products of 8 bf16 pairs (a packed uint4 each) added to acc in fp64,

@@ -140,14 +140,17 @@ struct Batch<kBf16, kB> {
 };
 
 // Steps per batch of the gate/up streams (register budget: ~64 VGPRs of raw
-// weights per matrix) and of the down stream (one matrix, twice the steps).
+// weights per matrix) and of the down stream (one matrix: FP4 twice the
+// steps; FP8 and bf16 twice the steps only with kDeep, for kernels whose
+// register budget holds 64 VGPRs of raw weights -- the split decode kernel's
+// 128-VGPR budget does not).  The batch size never changes the arithmetic.
 template <int F>
 constexpr int gate_up_batch() {
   return (F == kFp4E8M0 || F == kFp4F32) ? 8 : (F == kFp8Block ? 4 : 2);
 }
-template <int F>
+template <int F, bool kDeep = false>
 constexpr int down_batch() {
-  return (F == kFp4E8M0 || F == kFp4F32) ? 16 : gate_up_batch<F>();
+  return (F == kFp4E8M0 || F == kFp4F32 || kDeep) ? 2 * gate_up_batch<F>() : gate_up_batch<F>();
 }
 
 // Largest batch size <= kMax (a power of two) that divides n.
@@ -220,6 +223,39 @@ __device__ __forceinline__ void gate_up_slot(int fmt, const uint64_t* ent, const
   }
 }
 
+// One wave: rows r0..r0+15 of ONE of W1 / W3 (weights w, scales sc, [i][d])
+// over steps [st0, st1) against the m token rows of x: the same MFMA sequence
+// as that matrix's accumulator in gate_up_rows, so the sums are identical.
+template <int F, int kB>
+__device__ __forceinline__ void gate_or_up_rows(uint64_t w, uint64_t sc, const uint16_t* xs, int m, int d, int i,
+                                                int r0, int st0, int st1, f32x4& acc) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int row = r0 + r;
+  const Mat wm = make_mat<F>(w, sc, i, d);
+  for (int st = st0; st < st1; st += kB) {
+    Batch<F, kB> bw;
+    bw.load(wm, row, d, st, g);
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = mfma16x16x32(bw.frag(b, j, g), lds_frag(xs, d, r, g, st + b, j, m), acc);
+  }
+}
+
+// gate_or_up_rows with the largest batch (at most twice the gate/up batch:
+// one matrix instead of two) that divides the steps.
+template <int F>
+__device__ __forceinline__ void gate_or_up_any(uint64_t w, uint64_t sc, const uint16_t* xs, int m, int d, int i,
+                                               int r0, int st0, int st1, f32x4& acc) {
+  constexpr int kMax = 2 * gate_up_batch<F>();
+  const int b = batch_for<kMax>(st1 - st0);
+  if (b == kMax) gate_or_up_rows<F, kMax>(w, sc, xs, m, d, i, r0, st0, st1, acc);
+  else if (kMax > 8 && b == 8) gate_or_up_rows<F, (kMax > 8 ? 8 : 1)>(w, sc, xs, m, d, i, r0, st0, st1, acc);
+  else if (kMax > 4 && b == 4) gate_or_up_rows<F, (kMax > 4 ? 4 : 1)>(w, sc, xs, m, d, i, r0, st0, st1, acc);
+  else if (kMax > 2 && b == 2) gate_or_up_rows<F, (kMax > 2 ? 2 : 1)>(w, sc, xs, m, d, i, r0, st0, st1, acc);
+  else gate_or_up_rows<F, 1>(w, sc, xs, m, d, i, r0, st0, st1, acc);
+}
+
 // SwiGLU of the reference's M<=8 route (fused_moe.py:390-395) in fp32:
 // min(g, L) * sigmoid(min(g, L)) * clamp(u, -L, L); NaN passes both clamps.
 __device__ __forceinline__ float swiglu(float gsum, float usum, float L) {
@@ -254,10 +290,10 @@ __device__ __forceinline__ void down_rows(const uint64_t* ent, const uint16_t* a
   }
 }
 
-template <int F, typename Ready>
+template <int F, bool kDeep, typename Ready>
 __device__ __forceinline__ void down_any(const uint64_t* ent, const uint16_t* as, int m, int i, int d, int r0,
                                          f32x4& acc, Ready&& ready) {
-  constexpr int kMax = down_batch<F>();
+  constexpr int kMax = down_batch<F, kDeep>();
   const int b = batch_for<kMax>(i / 128);
   if (b == kMax) down_rows<F, kMax>(ent, as, m, i, d, r0, acc, ready);
   else if (kMax > 8 && b == 8) down_rows<F, (kMax > 8 ? 8 : 1)>(ent, as, m, i, d, r0, acc, ready);
@@ -266,14 +302,14 @@ __device__ __forceinline__ void down_any(const uint64_t* ent, const uint16_t* as
   else down_rows<F, 1>(ent, as, m, i, d, r0, acc, ready);
 }
 
-template <typename Ready>
+template <bool kDeep = false, typename Ready>
 __device__ __forceinline__ void down_slot(int fmt, const uint64_t* ent, const uint16_t* as, int m, int i, int d,
                                           int r0, f32x4& acc, Ready&& ready) {
   switch (fmt) {
-    case kFp4E8M0: down_any<kFp4E8M0>(ent, as, m, i, d, r0, acc, ready); break;
-    case kFp4F32: down_any<kFp4F32>(ent, as, m, i, d, r0, acc, ready); break;
-    case kFp8Block: down_any<kFp8Block>(ent, as, m, i, d, r0, acc, ready); break;
-    default: down_any<kBf16>(ent, as, m, i, d, r0, acc, ready); break;
+    case kFp4E8M0: down_any<kFp4E8M0, kDeep>(ent, as, m, i, d, r0, acc, ready); break;
+    case kFp4F32: down_any<kFp4F32, kDeep>(ent, as, m, i, d, r0, acc, ready); break;
+    case kFp8Block: down_any<kFp8Block, kDeep>(ent, as, m, i, d, r0, acc, ready); break;
+    default: down_any<kBf16, kDeep>(ent, as, m, i, d, r0, acc, ready); break;
   }
 }
 
@@ -295,6 +331,12 @@ __device__ __forceinline__ int load_agent(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ unsigned load_agent(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_agent(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ unsigned add_agent(unsigned* p, unsigned v) {
