@@ -63,30 +63,23 @@ static_assert(kMaxExperts == kThreads && kMaxExperts == 4 * 64, "plan build: one
 // that fix, cause not yet shown).  The entry point returns an error instead.
 constexpr bool kLayerKernelEnabled = true;
 
-// Control words (unsigned) at the start of the workspace.  Counters take the
-// atomic increments; waiters never poll a counter.  The producer that
-// completes a counter instead sets a flag, written in kFlagCopies copies 4 KiB
-// apart (workgroup b polls copy b % kFlagCopies), so that polling spreads over
-// several memory channels and never contends with the increments.
+// Control words (unsigned) at the start of the workspace.  Every handoff
+// between items is a tagged word (tag << 32 | fp32 bits, see launch_tag),
+// polled until it carries this launch's tag; the only counter counts the
+// workgroups that finished, so that the last one can advance the epoch.
 constexpr int kCtlEpoch = 0;     // tag of the previous launch (0: none yet)
 constexpr int kCtlDone = 128;    // workgroups finished
-constexpr int kCtlErr = 192;     // sticky: 1 + index of a control word whose wait gave up
-constexpr int kCtlSlot = 256;    // + 16*s: gate/up items of slot s finished
-constexpr int kCtlRowGroup = kCtlSlot + 16 * (kMaxSlots + 1);  // + g: down items of row group g finished
+constexpr int kCtlErr = 192;     // sticky: 1 + the code of a wait that gave up:
+constexpr int kWaitScores = 4608;  //   a plan's wait for the router scores
+constexpr int kWaitAct = 4609;     //   a down item's wait for its slot's activations
+constexpr int kWaitShared = 4610;  //   the shared down's wait for the gate and up sums
+constexpr int kWaitPart = 4611;    //   a row group's wait for the slots' partials
 constexpr int kMaxRowGroups = 2048;
-constexpr int kWaitScores = 4608;  // kCtlErr code (minus 1) of a plan's wait for the scores
-constexpr int kFlagCopies = 8;
-constexpr int kFlagBase = 8192;      // word index of flag copy 0 (32 KiB)
-constexpr int kFlagStride = 1024;    // words between copies (4 KiB)
-constexpr int kFlagSlot = 16;        // + 4*s: every gate/up item of slot s finished
-constexpr size_t kCtlBytes = 65536;
-static_assert(kCtlRowGroup + kMaxRowGroups <= kWaitScores, "control block overflow");
-// Router scores: kScoreCopies copies of [m][n_exp] words (tag << 32) | fp32
-// bits, each copy 4 KiB aligned, so that the workgroups polling them spread
-// over many memory channels.
+constexpr size_t kCtlBytes = 4096;
+// Router scores: kScoreCopies copies of [m][n_exp] tagged words, each copy
+// 4 KiB aligned, so that the workgroups polling them spread over many memory
+// channels.
 constexpr int kScoreCopies = 16;
-static_assert(kFlagSlot + 4 * (kMaxSlots + 1) <= kFlagStride, "flag block overflow");
-static_assert((kFlagBase + kFlagCopies * kFlagStride) * 4 <= (int)kCtlBytes, "flag copies overflow");
 
 struct LayerParams {
   const uint16_t* x;       // bf16 [m, d]
@@ -105,36 +98,13 @@ struct LayerParams {
   unsigned* ctl;
   uint64_t* scores;     // kScoreCopies copies of [m][n_exp] tagged fp32 scores
   int score_stride;     // 64-bit words between copies
-  float* act;   // fp32 [S][m][i] weighted activations of the routed slots
-  float* sgh;   // fp32 [2][m][i] shared expert gate (0) and up (1) row sums
-  float* part;  // fp32 [S + 1][m][d] per-slot down partials
+  uint64_t* act;   // tagged [S][m][i] weighted activations of the routed slots
+  uint64_t* sgh;   // tagged [2][m][i] shared expert gate (0) and up (1) row sums
+  uint64_t* part;  // tagged [S + 1][m][d] per-slot down partials (slot S: shared)
   // item ranges [start, end): R is [0, n_router); the others follow in an
   // order where every item's producers come before it
   int n_router, sgu0, sgu1, sd0, sd1, gu0, gu1, d0, d1, n_items;
 };
-
-// Waits (one thread) until this workgroup's copy of flag `flag` is set;
-// polls with backoff.  Gives up after kSpinLimit polls, recording the flag.
-__device__ bool wait_flag(unsigned* ctl, int flag) {
-  const unsigned* f = ctl + kFlagBase + (int)(blockIdx.x % kFlagCopies) * kFlagStride + flag;
-  int nap = 1;
-  for (unsigned it = 0; it < kSpinLimit; ++it) {
-    if (load_agent(f) != 0u) return true;
-    if (nap == 1) __builtin_amdgcn_s_sleep(1);
-    else if (nap == 2) __builtin_amdgcn_s_sleep(2);
-    else if (nap == 4) __builtin_amdgcn_s_sleep(4);
-    else if (nap == 8) __builtin_amdgcn_s_sleep(8);
-    else __builtin_amdgcn_s_sleep(16);
-    nap = nap < 16 ? 2 * nap : 16;
-  }
-  store_agent(ctl + kCtlErr, 1u + (unsigned)(kFlagBase + flag));
-  return false;
-}
-
-// Sets every copy of flag `flag` (after the data it announces is complete).
-__device__ __forceinline__ void set_flag(unsigned* ctl, int flag) {
-  for (int c = 0; c < kFlagCopies; ++c) store_agent(ctl + kFlagBase + c * kFlagStride + flag, 1u);
-}
 
 // This launch's tag: the previous launch's plus one (never 0).  The epoch word
 // changes only after every workgroup of the launch has finished its items.
@@ -143,6 +113,37 @@ __device__ __forceinline__ unsigned launch_tag(const unsigned* ctl) {
   return ep == 0xffffffffu ? 1u : ep + 1u;
 }
 __device__ __forceinline__ uint64_t tagged(unsigned tag, unsigned v) { return ((uint64_t)tag << 32) | v; }
+
+// Reads the tagged words ubase[j * jstride + off] (j < min(cnt, kN); ubase
+// and jstride the same in every lane, off the lane's own) into v once each
+// carries `tag`: every load of a round in flight at once, a lane re-reading
+// only the words it has not yet seen.  Gives up after kSpinLimit rounds,
+// recording `code` (the values it has not seen stay 0).
+template <int kN>
+__device__ __forceinline__ void poll_tagged(const uint64_t* ubase, int64_t jstride, uint32_t off, int cnt,
+                                            unsigned tag, float (&v)[kN], unsigned* ctl, int code) {
+  unsigned need = 0;
+#pragma unroll
+  for (int j = 0; j < kN; ++j) {
+    v[j] = 0.0f;
+    if (j < cnt) need |= 1u << j;
+  }
+  for (unsigned it = 0; it < kSpinLimit; ++it) {
+    const unsigned cur = need;
+    uint64_t w[kN];
+#pragma unroll
+    for (int j = 0; j < kN; ++j) w[j] = (cur >> j) & 1u ? load_agent(ubase + (int64_t)j * jstride + off) : 0ull;
+#pragma unroll
+    for (int j = 0; j < kN; ++j)
+      if (((cur >> j) & 1u) && (unsigned)(w[j] >> 32) == tag) {
+        v[j] = __uint_as_float((unsigned)w[j]);
+        need &= ~(1u << j);
+      }
+    if (__ballot(need != 0) == 0) return;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  if (need) store_agent(ctl + kCtlErr, 1u + (unsigned)code);
+}
 
 struct Shared {
   uint64_t ent[kMaxSlots + 1][6];     // table entry of routed slot s (and of the shared expert at slot S)
@@ -407,6 +408,7 @@ __device__ __noinline__ int gate_up_item(uint64_t kernarg, int q_arg, int state_
   const int s = qq / gu_per_slot;
   const int r0 = (qq % gu_per_slot) * kGuRows;
   if (s >= sh.n_routed) return state;
+  const unsigned tag = launch_tag(p.ctl);
   if (threadIdx.x < p.m) sh.wt_item[threadIdx.x] = sh.wt[s][threadIdx.x];
   const uint64_t* ent = sh.ent[s];
   ensure_x(p, state);
@@ -432,12 +434,8 @@ __device__ __noinline__ int gate_up_item(uint64_t kernarg, int q_arg, int state_
       usum = __fadd_rn(usum, sh.red[w][1][row * kMaxTok + col]);
     }
     const float a = __fmul_rn(sh.wt_item[col], swiglu(gsum, usum, p.limit));
-    store_agent(p.act + ((int64_t)s * p.m + col) * p.i + r0 + row, a);
+    store_agent(p.act + ((int64_t)s * p.m + col) * p.i + r0 + row, tagged(tag, __float_as_uint(a)));
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0 && add_agent(p.ctl + kCtlSlot + 16 * s, 1u) == (unsigned)(gu_per_slot - 1))
-    set_flag(p.ctl, kFlagSlot + 4 * s);
   return state;
 }
 
@@ -446,7 +444,6 @@ __device__ __noinline__ int gate_up_item(uint64_t kernarg, int q_arg, int state_
 // routed gate/up item in the same registers -- and publishes the rows' fp32
 // sums (the four waves' K ranges added in wave order, as gate_up_item adds
 // them) to p.sgh; the shared down applies the SwiGLU when it stages them.
-// The shared slot's flag is set after all 2 * i / 16 items.
 __device__ __noinline__ int shared_half_item(uint64_t kernarg, int q_arg, int state_arg) {
   const int q = __builtin_amdgcn_readfirstlane(q_arg);
   int state = __builtin_amdgcn_readfirstlane(state_arg);
@@ -454,6 +451,7 @@ __device__ __noinline__ int shared_half_item(uint64_t kernarg, int q_arg, int st
   Shared& sh = g_sh;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int k = q - p.sgu0, mat = k & 1, r0 = (k >> 1) * kGuRows;
+  const unsigned tag = launch_tag(p.ctl);
   const uint64_t* ent = sh.ent[p.S];
   ensure_x(p, state);
   const int per = (p.d / 128) / kWaves;
@@ -474,25 +472,18 @@ __device__ __noinline__ int shared_half_item(uint64_t kernarg, int q_arg, int st
     float sum = 0.0f;
 #pragma unroll
     for (int w4 = 0; w4 < kWaves; ++w4) sum = __fadd_rn(sum, sh.red[w4][0][row * kMaxTok + col]);
-    store_agent(p.sgh + ((int64_t)mat * p.m + col) * p.i + r0 + row, sum);
+    store_agent(p.sgh + ((int64_t)mat * p.m + col) * p.i + r0 + row, tagged(tag, __float_as_uint(sum)));
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0 && add_agent(p.ctl + kCtlSlot + 16 * p.S, 1u) == (unsigned)(2 * (p.i / kGuRows) - 1))
-    set_flag(p.ctl, kFlagSlot + 4 * p.S);
   return state;
 }
 
 // A run of routed gate/up items q, q + G, q + 2G, ... (G = grid) whose slots
 // are in format F with whole batches (d / 512 a multiple of the batch): as
 // soon as a wave has multiplied its last batch of item q it issues the first
-// batch of item q + G into the same registers, so the cross-wave reduction,
-// the publish and the wait for the stores of item q overlap the loads of the
-// next item.  The slot arrival of item q is counted after its stores are
-// complete; its result (is this the slot's last arrival?) is read one item
-// later, when the loads of the next item have returned anyway, and for the
-// run's last item at the end.  Same tiles and accumulation order as
-// gate_up_item, so the results are identical.  Returns the last item run.
+// batch of item q + G into the same registers, so the cross-wave reduction
+// and the tagged stores of item q overlap the loads of the next item.  Same
+// tiles and accumulation order as gate_up_item, so the results are
+// identical.  Returns the last item run.
 template <int F>
 __device__ __noinline__ int gate_up_run(uint64_t kernarg, int q_arg, int state_arg) {
   constexpr int kB = gate_up_batch<F>();
@@ -504,13 +495,12 @@ __device__ __noinline__ int gate_up_run(uint64_t kernarg, int q_arg, int state_a
   const int G = (int)gridDim.x, gu_per_slot = p.i / kGuRows;
   const int per = (p.d / 128) / kWaves, nb = per / kB, st0 = wave * per;
   ensure_x(p, state);
+  const unsigned tag = launch_tag(p.ctl);
   int s = (q - p.gu0) / gu_per_slot, r0 = ((q - p.gu0) % gu_per_slot) * kGuRows;
   Mat w1 = make_mat<F>(sh.ent[s][0], sh.ent[s][1], p.i, p.d), w3 = make_mat<F>(sh.ent[s][2], sh.ent[s][3], p.i, p.d);
   Batch<F, kB> b1, b3;
   b1.load(w1, r0 + r, p.d, st0, g);
   b3.load(w3, r0 + r, p.d, st0, g);
-  unsigned pend = 0;  // thread 0: counter value before the previous item's arrival
-  int pend_s = -1;
   for (;;) {
     if (threadIdx.x < p.m) sh.wt_item[threadIdx.x] = sh.wt[s][threadIdx.x];
     f32x4 ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
@@ -559,22 +549,15 @@ __device__ __noinline__ int gate_up_run(uint64_t kernarg, int q_arg, int state_a
           usum = __fadd_rn(usum, sh.red[w][1][row * kMaxTok + col]);
         }
         const float a = __fmul_rn(sh.wt_item[col], swiglu(gsum, usum, p.limit));
-        store_agent(p.act + ((int64_t)s * p.m + col) * p.i + r0 + row, a);
+        store_agent(p.act + ((int64_t)s * p.m + col) * p.i + r0 + row, tagged(tag, __float_as_uint(a)));
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // the stores of item q (and the next item's loads)
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      if (pend_s >= 0 && pend == (unsigned)(gu_per_slot - 1)) set_flag(p.ctl, kFlagSlot + 4 * pend_s);
-      pend = add_agent(p.ctl + kCtlSlot + 16 * s, 1u);
-      pend_s = s;
-    }
+    __syncthreads();  // sh.red and sh.wt_item are rewritten by the next item
     if (!next) break;
     q = q2;
     s = s2;
     r0 = r02;
   }
-  if (threadIdx.x == 0 && pend == (unsigned)(gu_per_slot - 1)) set_flag(p.ctl, kFlagSlot + 4 * pend_s);
   return q;
 }
 
@@ -588,79 +571,110 @@ __device__ __forceinline__ void down_slot_of(const LayerParams& p, int q, bool& 
 }
 
 // Down item q, first part: W2 rows of the slot against its activations, the
-// slot's fp32 partial sums written for the row group.  Needs the slot plan
-// for a routed slot only (the shared slot runs before the plan exists).
+// slot's fp32 partial sums published (tagged) for the row group.  Needs the
+// slot plan for a routed slot only (the shared slot may run before the plan
+// exists).  One instantiation per kind (routed or shared), so that each holds
+// only its own formats' registers.
+template <bool kShared>
 __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg) {
   const int q = __builtin_amdgcn_readfirstlane(q_arg);
   int state = __builtin_amdgcn_readfirstlane(state_arg);
   const LayerParams p = params(kernarg);
   Shared& sh = g_sh;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  bool is_shared;
+  bool is_shared_q;
   int s, g;
-  down_slot_of(p, q, is_shared, s, g);
+  down_slot_of(p, q, is_shared_q, s, g);
+  constexpr bool is_shared = kShared;
   if (!is_shared && s >= sh.n_routed) return state;
+  const unsigned tag = launch_tag(p.ctl);  // (issued before the weight loads)
   const uint64_t* ent = sh.ent[s];
   const int r0 = g * kDownRows + 16 * wave;
   const int m = p.m, i = p.i;
   unsigned* const ctl = p.ctl;
-  const float* const src = p.act + (int64_t)s * m * i;
-  const float* const sgh = p.sgh;
+  const uint64_t* const src = p.act + (int64_t)s * m * i;
+  const uint64_t* const sgh = p.sgh;
   const float limit = p.limit;
   f32x4 acc = {0, 0, 0, 0};
-  down_slot<true>(slot_format(p.scale_fmt, ent, is_shared), ent, g_tile, m, i, p.d, r0, acc, [&]() __attribute__((always_inline)) {
-    if (threadIdx.x == 0) wait_flag(ctl, kFlagSlot + 4 * s);
-    __syncthreads();
-    // fp32 activations -> bf16 hi rows [t][k] and lo rows [m + t][k]
-    // (8 loads in flight per thread before any is used); the shared slot's
-    // are the SwiGLU of its published gate and up sums (weight 1)
+  auto stage = [&]() __attribute__((always_inline)) {
+    // fp32 activations -> bf16 hi rows [t][k] and lo rows [m + t][k], each
+    // written once it carries this launch's tag;
+    // the shared slot's are the SwiGLU of its published gate and up sums
+    // (weight 1)
     const int n = m * i;
-    for (int c0 = threadIdx.x; c0 < n; c0 += 8 * kThreads) {
-      float a[8];
-      if (is_shared) {
-        float gv[8], uv[8];
+    constexpr int kStageWords = 4;  // per thread and round (registers: the W2 batch is live)
+    for (int u0 = 0; u0 < n; u0 += kStageWords * kThreads) {  // this thread's words u0 + threadIdx.x + kThreads * j
+      const int c0 = u0 + (int)threadIdx.x;
+      unsigned need = 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          gv[j] = (c0 + j * kThreads < n) ? load_agent(sgh + c0 + j * kThreads) : 0.0f;
-          uv[j] = (c0 + j * kThreads < n) ? load_agent(sgh + n + c0 + j * kThreads) : 0.0f;
+      for (int j = 0; j < kStageWords; ++j)
+        if (c0 + kThreads * j < n) need |= 1u << j;
+      for (unsigned it = 0; it < kSpinLimit; ++it) {
+        const unsigned cur = need;  // every load of the round in flight at once
+        uint64_t w[kStageWords], wu[kStageWords];
+#pragma unroll
+        for (int j = 0; j < kStageWords; ++j) {
+          const uint64_t* b = is_shared ? sgh : src;
+          w[j] = (cur >> j) & 1u ? load_agent(b + u0 + kThreads * j + threadIdx.x) : 0ull;
+          wu[j] = is_shared && ((cur >> j) & 1u) ? load_agent(sgh + n + u0 + kThreads * j + threadIdx.x) : 0ull;
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] = __fmul_rn(1.0f, swiglu(gv[j], uv[j], limit));
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] = (c0 + j * kThreads < n) ? load_agent(src + c0 + j * kThreads) : 0.0f;
+        for (int j = 0; j < kStageWords; ++j) {
+          const bool fresh = (unsigned)(w[j] >> 32) == tag && (!is_shared || (unsigned)(wu[j] >> 32) == tag);
+          if (((cur >> j) & 1u) && fresh) {
+            const float v = __uint_as_float((unsigned)w[j]);
+            const float a = is_shared ? __fmul_rn(1.0f, swiglu(v, __uint_as_float((unsigned)wu[j]), limit)) : v;
+            const int c = c0 + kThreads * j;
+            const uint32_t hi = f32_to_bf16_bits(a);
+            const uint32_t lo = f32_to_bf16_bits(__fadd_rn(a, -bf16_bits_to_f32(hi)));
+            g_tile[c] = (uint16_t)hi;
+            g_tile[n + c] = (uint16_t)lo;
+            need &= ~(1u << j);
+          }
+        }
+        if (__ballot(need != 0) == 0) break;
+        __builtin_amdgcn_s_sleep(2);
       }
+      if (need) {  // gave up: zeros in the tile, the wait recorded
+        store_agent(ctl + kCtlErr, 1u + (unsigned)(is_shared ? kWaitShared : kWaitAct));
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int c = c0 + j * kThreads;
-        if (c < n) {
-          const uint32_t hi = f32_to_bf16_bits(a[j]);
-          const uint32_t lo = f32_to_bf16_bits(__fadd_rn(a[j], -bf16_bits_to_f32(hi)));
-          g_tile[c] = (uint16_t)hi;
-          g_tile[n + c] = (uint16_t)lo;
-        }
+        for (int j = 0; j < kStageWords; ++j)
+          if ((need >> j) & 1u) {
+            g_tile[c0 + kThreads * j] = 0;
+            g_tile[n + c0 + kThreads * j] = 0;
+          }
       }
     }
     __syncthreads();
-  });
+  };
+  const int fmt = slot_format(p.scale_fmt, ent, is_shared);
+  if constexpr (kShared) {
+    if (fmt == kFp8Block) down_any<kFp8Block, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
+    else down_any<kBf16, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
+  } else {
+    if (fmt == kFp4E8M0) down_any<kFp4E8M0, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
+    else if (fmt == kFp4F32) down_any<kFp4F32, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
+    else down_any<kBf16, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
+  }
   state = 0;
   // lane (col = lane%16) holds rows 4*(lane/16)+c; column t (hi) + column m+t (lo)
   // of token t are combined through the lane that owns column t.
-  float* part = p.part + (int64_t)s * m * p.d;
+  uint64_t* part = p.part + (int64_t)s * m * p.d;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int col = lane & 15;
     const float lo = __shfl(acc[c], (lane & 48) | ((col + m) & 15), 64);
-    if (col < m) store_agent(part + (int64_t)col * p.d + r0 + 4 * (lane >> 4) + c, __fadd_rn(acc[c], lo));
+    if (col < m)
+      store_agent(part + (int64_t)col * p.d + r0 + 4 * (lane >> 4) + c, tagged(tag, __float_as_uint(__fadd_rn(acc[c], lo))));
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
   return state;
 }
 
-// Down item q, second part (the slot plan exists): arrival on the row group;
-// the last slot to arrive adds the slots' partials in slot order (routed
-// ascending, shared last) and writes the output rows.
+// Down item q, second part (the slot plan exists): of the row group's
+// contributors (its down item of each routed slot, and the shared down), the
+// one with the largest item index -- it waits only for smaller ones -- adds
+// the slots' tagged partials in slot order (routed ascending, shared last)
+// and writes the output rows.
 __device__ __noinline__ void down_finish(uint64_t kernarg, int q_arg) {
   const int q = __builtin_amdgcn_readfirstlane(q_arg);
   const LayerParams p = params(kernarg);
@@ -670,15 +684,32 @@ __device__ __noinline__ void down_finish(uint64_t kernarg, int q_arg) {
   down_slot_of(p, q, is_shared, s, g);
   const int n_routed = sh.n_routed;
   if (!is_shared && s >= n_routed) return;
+  const int dps = p.d / kDownRows;
+  int last = n_routed > 0 ? p.d0 + (n_routed - 1) * dps + g : -1;
+  if (p.shared && p.sd0 + g > last) last = p.sd0 + g;
+  if (q != last) return;
+  const unsigned tag = launch_tag(p.ctl);
   const int m = p.m;
-  const int n_slots = n_routed + (p.shared ? 1 : 0);
-  if (threadIdx.x == 0) sh.flag = add_agent(p.ctl + kCtlRowGroup + g, 1u) == (unsigned)(n_slots - 1);
-  __syncthreads();
-  if (sh.flag) {
-    for (int c = threadIdx.x; c < kDownRows * m; c += kThreads) {
-      const int t = c / kDownRows, dd = g * kDownRows + (c - t * kDownRows);
-      const float v = sum_slots_agent(p.part + (int64_t)t * p.d + dd, (int64_t)m * p.d, n_routed,
-                                      p.shared ? p.part + ((int64_t)p.S * m + t) * p.d + dd : nullptr);
+  const int64_t stride = (int64_t)m * p.d;  // between slots
+  for (int c0 = 0; c0 < kDownRows * m; c0 += kThreads) {
+    const int c = c0 + (int)threadIdx.x;
+    const bool mine = c < kDownRows * m;
+    const int t = mine ? c / kDownRows : 0, dd = g * kDownRows + (mine ? c - t * kDownRows : 0);
+    const uint32_t off = (uint32_t)(t * p.d + dd);
+    float v = 0.0f;
+    for (int s0 = 0; s0 < n_routed; s0 += 8) {
+      float pv[8];
+      poll_tagged<8>(p.part + (int64_t)s0 * stride, stride, off, mine ? n_routed - s0 : 0, tag, pv, p.ctl, kWaitPart);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < n_routed) v = __fadd_rn(v, pv[j]);
+    }
+    if (p.shared) {
+      float pv[1];
+      poll_tagged<1>(p.part + (int64_t)p.S * stride, stride, off, mine ? 1 : 0, tag, pv, p.ctl, kWaitPart);
+      v = __fadd_rn(v, pv[0]);
+    }
+    if (mine) {
       const int64_t o = (int64_t)t * p.d + dd;
       if (p.out_f32) p.out_f32[o] = v;
       if (p.out_bf16) p.out_bf16[o] = (uint16_t)f32_to_bf16_bits(v);
@@ -703,7 +734,7 @@ __global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
       continue;
     }
     if (q >= p.sd0 && q < p.sd1) {  // shared down: the plan is needed only for its arrival
-      state = down_item(kernarg, q, state);
+      state = down_item<true>(kernarg, q, state);
       if (!g_sh.have_plan) plan_item(kernarg);
       down_finish(kernarg, q);
       continue;
@@ -723,7 +754,7 @@ __global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
         state = gate_up_item(kernarg, q, state);
       }
     } else {
-      state = down_item(kernarg, q, state);
+      state = down_item<false>(kernarg, q, state);
       down_finish(kernarg, q);
     }
   }
@@ -732,30 +763,21 @@ __global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
   // that needs the plan (the plan waits only for R items, which wait for
   // nothing)
   if (blockIdx.x == gridDim.x - 1 && !g_sh.have_plan) plan_item(kernarg);
-  // the last workgroup to finish re-arms every control word for the next call
-  // and advances the epoch to this launch's tag
+  // the last workgroup to finish (every workgroup has read the epoch by then)
+  // advances the epoch to this launch's tag and re-arms the counter
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) g_sh.flag = add_agent(p.ctl + kCtlDone, 1u) == gridDim.x - 1;
-  __syncthreads();
-  if (!g_sh.flag) return;
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == 0 && add_agent(p.ctl + kCtlDone, 1u) == gridDim.x - 1) {
     store_agent(p.ctl + kCtlEpoch, launch_tag(p.ctl));
     store_agent(p.ctl + kCtlDone, 0u);
-  }
-  for (int s = threadIdx.x; s <= p.S; s += kThreads) store_agent(p.ctl + kCtlSlot + 16 * s, 0u);
-  for (int g = threadIdx.x; g < p.d / kDownRows; g += kThreads) store_agent(p.ctl + kCtlRowGroup + g, 0u);
-  for (int c = threadIdx.x; c < kFlagCopies * (p.S + 1); c += kThreads) {
-    const int copy = c % kFlagCopies, s = c / kFlagCopies;  // slot s (S: the shared slot)
-    store_agent(p.ctl + kFlagBase + copy * kFlagStride + kFlagSlot + 4 * s, 0u);
   }
 }
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 int64_t score_stride_words(int64_t m, int64_t n_exp) { return (m * n_exp * 8 + 4095) / 4096 * 512; }
 size_t scores_bytes(int64_t m, int64_t n_exp) { return (size_t)kScoreCopies * score_stride_words(m, n_exp) * 8; }
-size_t act_bytes(int64_t m, int64_t i, int top_k) { return align256((size_t)(m * top_k + 2) * m * i * 4); }
-size_t part_bytes(int64_t m, int64_t d, int top_k) { return align256((size_t)(m * top_k + 1) * m * d * 4); }
+size_t act_bytes(int64_t m, int64_t i, int top_k) { return align256((size_t)(m * top_k + 2) * m * i * 8); }
+size_t part_bytes(int64_t m, int64_t d, int top_k) { return align256((size_t)(m * top_k + 1) * m * d * 8); }
 
 // Workgroups of moe_layer_kernel the device holds at once, for an LDS size.
 int resident_workgroups(size_t lds, int* out) {
@@ -856,10 +878,10 @@ extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64
   p.scores = (uint64_t*)ws;
   p.score_stride = (int)score_stride_words(m, n_experts);
   ws += scores_bytes(m, n_experts);
-  p.act = (float*)ws;
+  p.act = (uint64_t*)ws;
   p.sgh = p.act + (size_t)p.S * m * i;
   ws += act_bytes(m, i, top_k);
-  p.part = (float*)ws;
+  p.part = (uint64_t*)ws;
   const int has_shared = shared ? 1 : 0;
   p.n_router = (int)n_experts;
   // Item order after R (producers always before their consumers): SGU, SD,
