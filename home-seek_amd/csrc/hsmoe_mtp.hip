@@ -6,8 +6,11 @@
 //   pred[t]; the bonus row is the first mismatch (or the last row).
 // Each logit is the correctly rounded bf16 of the exact dot product: one lane
 // owns one vocab row and sums it in fp64 (bf16 x bf16 products are exact in
-// fp64); the hidden states are pre-widened to fp64 and read with uniform
-// (scalar) loads, so the per-weight cost is 2 conversions + n_tok fp64 FMAs.
+// fp64); the hidden states are pre-widened to fp64, and each workgroup copies
+// them into LDS when they fit (n_tok * d * 8 <= kLdsHBytes), so that the
+// inner loop reads them with broadcast LDS loads instead of scalar loads that
+// stall on the scalar cache; the per-weight cost is 2 conversions + n_tok
+// fp64 FMAs.
 // The vocab-wide argmax is a 64-bit atomic max on (orderable logit, ~index);
 // the last workgroup to finish evaluates the acceptance rule and clears the
 // counters for the next call.
@@ -18,8 +21,9 @@ namespace hsmoe {
 namespace {
 
 constexpr int kMaxTok = 8;
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kRowsPerBlock = 64 * kWaves;
+constexpr size_t kLdsHBytes = 128 * 1024;  // hidden states in LDS up to this size (one workgroup per CU)
 
 struct Workspace {
   unsigned long long key[kMaxTok];
@@ -42,14 +46,21 @@ __device__ __forceinline__ unsigned long long logit_key(uint32_t bits, int64_t v
   return ((unsigned long long)o << 32) | (unsigned long long)(0xffffffffu - (uint32_t)v);
 }
 
-template <int kTok>
+extern __shared__ double s_h[];  // [kTok][d] when kLds
+
+template <int kTok, bool kLds>
 __global__ void __launch_bounds__(64 * kWaves)
-    lm_head_kernel(const uint16_t* __restrict__ w, const double* __restrict__ h64, int64_t d, int64_t vocab,
+    lm_head_kernel(const uint16_t* __restrict__ w, const double* __restrict__ h64g, int64_t d, int64_t vocab,
                    const int64_t* __restrict__ ids, uint16_t* __restrict__ logits, int64_t* __restrict__ pred_out,
                    int64_t* __restrict__ result_out, Workspace* __restrict__ ws) {
   __shared__ unsigned long long s_key[kWaves][kTok];
   __shared__ int s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if constexpr (kLds) {
+    for (int64_t c = threadIdx.x; c < kTok * d; c += 64 * kWaves) s_h[c] = h64g[c];
+    __syncthreads();
+  }
+  const double* __restrict__ h64 = kLds ? s_h : h64g;
   const int64_t v = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x;
   const bool on = v < vocab;
   const uint16_t* wr = w + (on ? v : 0) * d;
@@ -120,8 +131,21 @@ template <int kTok>
 int launch(const uint16_t* w, const double* h64, int64_t d, int64_t vocab, const int64_t* ids, uint16_t* logits,
            int64_t* pred, int64_t* result, Workspace* ws, hipStream_t st) {
   const unsigned nb = (unsigned)((vocab + kRowsPerBlock - 1) / kRowsPerBlock);
-  hipLaunchKernelGGL(lm_head_kernel<kTok>, dim3(nb), dim3(64 * kWaves), 0, st, w, h64, d, vocab, ids, logits, pred,
-                     result, ws);
+  const size_t lds = (size_t)kTok * (size_t)d * 8;
+  if (lds <= kLdsHBytes) {
+    static bool raised = false;  // allow more than the default dynamic LDS (once per process)
+    if (!raised) {
+      if (hipFuncSetAttribute((const void*)lm_head_kernel<kTok, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)kLdsHBytes) != hipSuccess)
+        return fail(HSMOE_ERR_LAUNCH, "hsmoe_lm_head_accept: could not allow %zu bytes of LDS", kLdsHBytes);
+      raised = true;
+    }
+    hipLaunchKernelGGL((lm_head_kernel<kTok, true>), dim3(nb), dim3(64 * kWaves), lds, st, w, h64, d, vocab, ids,
+                       logits, pred, result, ws);
+  } else {
+    hipLaunchKernelGGL((lm_head_kernel<kTok, false>), dim3(nb), dim3(64 * kWaves), 0, st, w, h64, d, vocab, ids,
+                       logits, pred, result, ws);
+  }
   return check_launch("hsmoe_lm_head_accept");
 }
 
