@@ -67,10 +67,8 @@ __global__ void __launch_bounds__(64 * kWaves)
   double acc[kTok];
 #pragma unroll
   for (int t = 0; t < kTok; ++t) acc[t] = 0.0;
-  for (int64_t k0 = 0; k0 < d; k0 += 64) {
-    uint4 q[8];
-#pragma unroll
-    for (int b = 0; b < 8; ++b) q[b] = *reinterpret_cast<const uint4*>(wr + k0 + 8 * b);
+  // 8 x 16 B of the row (64 weights) per lane, summed in k order
+  auto consume = [&](const uint4 (&q)[8], int64_t k0) __attribute__((always_inline)) {
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       const uint32_t qq[4] = {q[b].x, q[b].y, q[b].z, q[b].w};
@@ -81,6 +79,33 @@ __global__ void __launch_bounds__(64 * kWaves)
 #pragma unroll
         for (int t = 0; t < kTok; ++t) acc[t] = __fma_rn(h64[t * d + k0 + 8 * b + e], wv, acc[t]);
       }
+    }
+  };
+  auto load = [&](uint4 (&q)[8], int64_t k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int b = 0; b < 8; ++b) q[b] = *reinterpret_cast<const uint4*>(wr + k0 + 8 * b);
+  };
+  uint4 qa[8], qb[8];
+  if constexpr (kTok == 1) {
+    // one token: little arithmetic per byte, so the next 64 weights are
+    // loaded while the current ones are summed (measured: 189 -> 181 us for
+    // a 129,280 x 4096 head)
+    load(qa, 0);
+    for (int64_t k0 = 0; k0 < d; k0 += 128) {  // d is a multiple of 512
+      load(qb, k0 + 64);
+      consume(qa, k0);
+      if (k0 + 128 < d) load(qa, k0 + 128);
+      consume(qb, k0 + 64);
+    }
+  } else {
+    // several tokens: the FMAs dominate; 128 weights loaded per step, then
+    // summed (measured at 3 tokens: 269 -> 260 us; the pipelined form above
+    // runs out of registers there)
+    for (int64_t k0 = 0; k0 < d; k0 += 128) {
+      load(qa, k0);
+      load(qb, k0 + 64);
+      consume(qa, k0);
+      consume(qb, k0 + 64);
     }
   }
 #pragma unroll
