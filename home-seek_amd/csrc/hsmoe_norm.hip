@@ -6,7 +6,8 @@
 //   h = bf16(h + res)      the attention stand-in residual of this layer
 // One workgroup (256 threads) per row.  Each thread owns 8-column chunks
 // c, c + 256, ...; the row stays in LDS between the sum-of-squares pass and
-// the scaling pass, so x is read from memory once.  The sum of squares is
+// the scaling pass, so x is read from memory once; the weight row is loaded
+// into LDS in the first pass too, so that the scaling pass waits on no memory.  The sum of squares is
 // accumulated per thread in column order, then reduced across the wave by a
 // fixed xor-butterfly and across the 4 waves in wave order: results are
 // deterministic.
@@ -26,12 +27,14 @@ __global__ void __launch_bounds__(kThreads)
                         const uint4* __restrict__ w, int64_t d, float eps, uint4* __restrict__ h_out,
                         uint4* __restrict__ out) {
   __shared__ uint4 row[kMaxD / 8];
+  __shared__ uint4 wrow[kMaxD / 8];
   __shared__ float part[kThreads / 64];
   const int chunks = (int)(d / 8);
   const int64_t base = (int64_t)blockIdx.x * chunks;
   float s = 0.0f;
   for (int c = threadIdx.x; c < chunks; c += kThreads) {
     uint4 v = x[base + c];
+    wrow[c] = w[c];
     if (kAdd) v = norm_add_chunk(v, add[base + c]);
     if (kRes) v = norm_add_chunk(v, res[c]);
     if (h_out) h_out[base + c] = v;
@@ -42,7 +45,7 @@ __global__ void __launch_bounds__(kThreads)
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
   __syncthreads();
   const float inv = norm_inv(part, d, eps);
-  for (int c = threadIdx.x; c < chunks; c += kThreads) out[base + c] = norm_scale_chunk(row[c], w[c], inv);
+  for (int c = threadIdx.x; c < chunks; c += kThreads) out[base + c] = norm_scale_chunk(row[c], wrow[c], inv);
 }
 
 }  // namespace
