@@ -58,10 +58,6 @@ constexpr int kDownRows = 16 * kWaves;
 constexpr int kRtChunks = 8192 / 8 / kThreads;  // 16-byte gate-row chunks per thread (d <= 8192)
 constexpr unsigned kSpinLimit = 1u << 16;
 static_assert(kMaxExperts == kThreads && kMaxExperts == 4 * 64, "plan build: one expert per thread, four per lane");
-// Off: the launch faulted the GPU on MI355X (first with the parameters read
-// through a null kernarg pointer in the item functions, then once more after
-// that fix, cause not yet shown).  The entry point returns an error instead.
-constexpr bool kLayerKernelEnabled = true;
 
 // Control words (unsigned) at the start of the workspace.  Every handoff
 // between items is a tagged word (tag << 32 | fp32 bits, see launch_tag),
@@ -829,10 +825,6 @@ extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64
                                       void* logits_out, float* out_f32, void* out_bf16, void* workspace,
                                       size_t workspace_bytes, hsmoe_stream_t stream) {
   const char* name = "hsmoe_moe_layer_decode";
-  if (!kLayerKernelEnabled)
-    return fail(HSMOE_ERR_LAUNCH,
-                "%s: disabled -- this persistent kernel faulted the GPU on its first runs and stays off until the "
-                "cause is shown; use hsmoe_router_topk + hsmoe_moe_decode", name);
   if (!x || !gate_w || !expert_table || !topk_idx_out || !topk_w_out || (!out_f32 && !out_bf16))
     return fail(HSMOE_ERR_ARG, "%s: null pointer or no output", name);
   if (scale_kind != HSMOE_SCALE_E8M0 && scale_kind != HSMOE_SCALE_F32)

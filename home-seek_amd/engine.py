@@ -74,12 +74,19 @@ class HomeSeekMoEEngine:
             return None
 
     def _load_expert_weights(self, layer_idx: int, eid: int):
-        """((w1, s1, fmt), (w3, s3, fmt), (w2, s2, fmt)) with fmt "fp4_gpu" (engine.py:1084-1129)."""
+        """((w1, s1, fmt), (w3, s3, fmt), (w2, s2, fmt)) with fmt "fp4_gpu" (engine.py:1084-1129).
+
+        As the reference's on-device entries (_make_raw_entry, engine.py:1054-1082),
+        the data are the store's int8 views and the scales are fp32 (the E8M0
+        values, 2^(e-127), converted by torch's float8_e8m0fnu cast: a new
+        tensor of 4 bytes per scale).  The decode kernels read the store's E8M0
+        bytes directly through the layer's table, not these entries."""
         raw = self._load_expert_fp4_raw(layer_idx, eid)
         if raw is None:
             return None
         w1, s1, w3, s3, w2, s2 = raw
-        return (w1, s1, "fp4_gpu"), (w3, s3, "fp4_gpu"), (w2, s2, "fp4_gpu")
+        return ((w1, s1.to(torch.float32), "fp4_gpu"), (w3, s3.to(torch.float32), "fp4_gpu"),
+                (w2, s2.to(torch.float32), "fp4_gpu"))
 
     _load_expert_raw = _load_expert_weights
 
@@ -180,7 +187,13 @@ class HomeSeekMoEEngine:
             self._phase = "verify"
             _, hf = self._forward_stack(combined)
             logits, pred, result = ops.lm_head_accept(hf, self.lm_head, combined.reshape(-1))
-            n_accept, bonus_row = (int(v) for v in result.tolist())  # the one host sync per verify
+            # the one host sync per verify also reads the layer kernels' status words
+            words = [w.to(torch.int64) for w in ops.moe_layer_status_words(self.device)]
+            vals = torch.cat([result] + words).tolist()
+            if any(vals[2:]):
+                raise ops._lib.HsmoeError(f"moe_layer_kernel: a cross-workgroup wait gave up (status "
+                                          f"{max(vals[2:])}); this verify's outputs are not valid")
+            n_accept, bonus_row = vals[0], vals[1]
             bonus_logits = logits[bonus_row:bonus_row + 1]
         finally:
             self._global_pos = pos_bak + n_accept
@@ -242,18 +255,36 @@ class HomeSeekMoEEngine:
             h = h + pending
         return h, (self._final_hidden(h) if final_norm else None)
 
+    def draft_count(self) -> int:
+        """Drafts per decode step: config.mtp_num_draft when the MTP block, the
+        embedding and lm_head are present, else 0 (plain greedy decode)."""
+        has_mtp = self._mtp_weights is not None and self.embed is not None and self.lm_head is not None
+        return max(0, int(self.config.mtp_num_draft)) if has_mtp else 0
+
     @torch.no_grad()
     def decode_step(self, cur: torch.Tensor, out_row: torch.Tensor | None = None):
-        """One greedy decode step with MTP verify, on the device only
-        (engine.py:2809-2922 at temperature 0): M=1 forward of `cur` -> main
-        token A; drafts [d0, d1]; verify [A, d0, d1]; n = accepted drafts.
-        Returns (row [4] = A, d0, d1, bonus token; count of tokens emitted =
-        1 + (n > 0) * (n + 1); next token to forward; n), all device tensors."""
+        """One greedy decode step, on the device only (engine.py:2809-2922 at
+        temperature 0): M=1 forward of `cur` -> main token A; with n_draft =
+        draft_count() > 0, drafts [d_0 .. d_{n_draft-1}] from the MTP block and
+        one verify of [A, drafts]; n = accepted drafts.  Returns (row
+        [2 + n_draft] = A, drafts, bonus token (row [1] = A without drafts);
+        count of tokens emitted = 1 + (n > 0) * (n + 1); next token to forward
+        (the bonus when n > 0, else A, which the next step forwards as the
+        reference's loop does); n), all device tensors."""
         cur = cur.reshape(1, 1)
         h, hf = self._forward_stack(cur)
         _, pred, _ = ops.lm_head_accept(hf, self.lm_head, None, want_logits=False)
         a = pred.reshape(1, 1)
-        drafts, n_draft = self._mtp_generate_draft(h, self.config.mtp_num_draft, 0.0, last_token_id=a)
+        n_draft = self.draft_count()
+        drafts = None
+        if n_draft > 0:
+            drafts, n_draft = self._mtp_generate_draft(h, n_draft, 0.0, last_token_id=a)
+        if drafts is None or n_draft == 0:
+            row = a.reshape(1)
+            if out_row is not None:
+                out_row.copy_(row)
+            one = torch.ones((), dtype=torch.int64, device=a.device)
+            return row, one, a.reshape(()), torch.zeros_like(one)
         combined = torch.cat([a, drafts], dim=-1)
         _, hfv = self._forward_stack(combined)
         _, pred_v, result = ops.lm_head_accept(hfv, self.lm_head, combined.reshape(-1), want_logits=False)
@@ -294,7 +325,7 @@ class HomeSeekMoEEngine:
 
 class GreedyDecoder:
     """Device-resident greedy decode loop with MTP verify (engine.py:2809-2922 at
-    temperature 0).  Per step it records the row [A, d0, d1, bonus], the count of
+    temperature 0).  Per step it records the row [A, drafts, bonus], the count of
     tokens emitted and the accepted drafts into device buffers of `capacity`
     steps, and carries the next token on the device; with graph=True one step
     is captured as a HIP graph (after one eager warm-up step, so that every
@@ -305,7 +336,8 @@ class GreedyDecoder:
         if capacity < 1:
             raise ValueError("a decoder needs room for at least one step")
         self.engine, self.capacity = engine, int(capacity)
-        self.rows = torch.zeros(self.capacity, 4, dtype=torch.int64, device=dev)
+        self.width = 2 + engine.draft_count() if engine.draft_count() > 0 else 1  # A, drafts, bonus
+        self.rows = torch.zeros(self.capacity, self.width, dtype=torch.int64, device=dev)
         self.counts = torch.zeros(self.capacity, dtype=torch.int64, device=dev)
         self.n_accs = torch.zeros(self.capacity, dtype=torch.int64, device=dev)
         self.cur = torch.zeros(1, 1, dtype=torch.int64, device=dev)
@@ -326,7 +358,7 @@ class GreedyDecoder:
     def _body(self):
         row, count, nxt, n_acc = self.engine.decode_step(self.cur)
         at = self.k.reshape(1)
-        self.rows.index_copy_(0, at, row.reshape(1, 4))
+        self.rows.index_copy_(0, at, row.reshape(1, self.width))
         self.counts.index_copy_(0, at, count.reshape(1))
         self.n_accs.index_copy_(0, at, n_acc.reshape(1))
         self.cur.copy_(nxt.reshape(1, 1))
@@ -350,14 +382,17 @@ class GreedyDecoder:
         self.done += n
 
     def result(self):
-        """(tokens emitted, accepted drafts per step) of the rows written since reset()."""
+        """(tokens emitted, accepted drafts per step) of the rows written since
+        reset().  Raises HsmoeError when a layer launch of the run reported a
+        cross-workgroup wait that gave up (its outputs are not valid)."""
+        ops.check_moe_layer_status(self.engine.device)
         n = self.done
         rows_h, counts_h = self.rows[:n].cpu().tolist(), self.counts[:n].cpu().tolist()
         tokens = []
         for r, c in zip(rows_h, counts_h):
             tokens.append(r[0])
             if c > 1:
-                tokens.extend(r[1:c - 1] + [r[3]])
+                tokens.extend(r[1:c - 1] + [r[-1]])
         return tokens, self.n_accs[:n].cpu().tolist()
 
 

@@ -14,14 +14,24 @@ from ._lib import SCALE_E8M0, SCALE_F32, check, lib, ptr, require_cuda, stream_p
 
 __all__ = [
     "SCALE_E8M0", "SCALE_F32", "scale_kind_of", "fp4_dequant_bf16", "fp8_dequant_bf16", "router_topk",
-    "moe_decode", "moe_layer_decode", "moe_layer_status", "lm_head_accept", "expert_table", "shared_entry",
-    "MAX_DECODE_TOKENS", "MAX_LAYER_EXPERTS",
+    "moe_decode", "moe_layer_decode", "moe_layer_status", "moe_layer_status_words", "lm_head_accept", "expert_table",
+    "shared_entry", "MAX_DECODE_TOKENS", "MAX_LAYER_EXPERTS",
 ]
 
 MAX_DECODE_TOKENS = 8
 MAX_LAYER_EXPERTS = 256  # expert count the one-launch layer kernel handles
 
 _workspaces: dict[tuple, torch.Tensor] = {}
+_layer_launches: dict[tuple, int] = {}  # eager layer launches per workspace since it was zeroed
+
+# The layer kernel tags every cross-workgroup word with its launch number (a
+# 32-bit epoch kept in the workspace), so a workspace must be zeroed again
+# before 2^32 launches; it is re-armed (zeroed once its epoch passes 2^31) by
+# moe_layer_status, which reads the epoch, and every _REARM_CHECK_EVERY eager
+# launches.  Graph replays are not counted: a replay loop reads the status
+# (GreedyDecoder.result does) at least once per 2^31 launches.
+_REARM_EPOCH = 1 << 31
+_REARM_CHECK_EVERY = 1 << 24
 
 
 def _workspace(device: torch.device, purpose: str, nbytes: int) -> torch.Tensor:
@@ -257,6 +267,11 @@ def moe_layer_decode(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Ten
     logits = torch.empty(m, n_exp, dtype=torch.bfloat16, device=dev) if want_logits else None
     nbytes = lib().hsmoe_moe_layer_workspace_size(m, d, i, n_exp, top_k)
     ws = _workspace(dev, "layer", nbytes)
+    key = (dev.index, stream_ptr(dev), "layer")
+    n = _layer_launches.get(key, 0) + 1
+    _layer_launches[key] = n
+    if n % _REARM_CHECK_EVERY == 0 and not torch.cuda.is_current_stream_capturing():
+        _rearm_if_old(ws)
     rc = lib().hsmoe_moe_layer_decode(ptr(x), m, d, i, ptr(gate_w), ptr(gate_bias), n_exp, top_k, scaling,
                                       ptr(table), scale_kind, ptr(shared), swiglu_limit, ptr(idx_out), ptr(w_out),
                                       ptr(logits), ptr(out_f32), ptr(out_bf16), ptr(ws), ws.numel(),
@@ -266,15 +281,51 @@ def moe_layer_decode(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Ten
     return res + (logits,) if want_logits else res
 
 
-def moe_layer_status(device: torch.device | None = None) -> int:
-    """The layer kernel's status word in this stream's workspace (0 = every
-    cross-workgroup wait completed).  Synchronises the device."""
+def _layer_workspaces(device: torch.device, stream: int | None = None) -> list[torch.Tensor]:
+    return [ws for (d, st, purpose), ws in _workspaces.items()
+            if purpose == "layer" and d == device.index and (stream is None or st == stream)]
+
+
+def moe_layer_status_words(device: torch.device | None = None, stream: int | None = None) -> list[torch.Tensor]:
+    """int32 [1] device views of the layer kernel's sticky status word in the
+    layer workspaces of `stream` (a raw stream handle), or of every stream of
+    the device (a decode graph's capture stream included) when None."""
     device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
-    ws = _workspaces.get((device.index, stream_ptr(device), "layer"))
-    if ws is None:
-        return 0
     off = lib().hsmoe_moe_layer_status_offset()
-    return int(ws[off:off + 4].view(torch.int32).item())
+    return [ws[off:off + 4].view(torch.int32) for ws in _layer_workspaces(device, stream)]
+
+
+def _rearm_if_old(ws: torch.Tensor) -> None:
+    """Zeroes a layer workspace whose epoch passed 2^31 (synchronises the device)."""
+    epoch = int(ws[0:4].view(torch.int32).item()) & 0xFFFFFFFF
+    if epoch >= _REARM_EPOCH:
+        torch.cuda.synchronize(ws.device)
+        ws.zero_()
+
+
+def moe_layer_status(device: torch.device | None = None, stream: int | None = None) -> int:
+    """The layer kernel's sticky status word: 0 when every cross-workgroup wait
+    of every launch completed, else 1 + the code of a wait that gave up (the
+    outputs of that launch are not valid).  Reads the workspaces of `stream`,
+    or of every stream of the device when None, and re-arms a workspace whose
+    launch epoch is old.  Synchronises the device."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    words = moe_layer_status_words(device, stream)
+    status = 0
+    for w in words:
+        status = status or int(w.item())
+    if not torch.cuda.is_current_stream_capturing():
+        for ws in _layer_workspaces(device, stream):
+            _rearm_if_old(ws)
+    return status
+
+
+def check_moe_layer_status(device: torch.device | None = None, stream: int | None = None) -> None:
+    """Raises HsmoeError when moe_layer_status is not 0."""
+    st = moe_layer_status(device, stream)
+    if st:
+        raise _lib.HsmoeError(f"moe_layer_kernel: a cross-workgroup wait gave up (status {st}); "
+                              "the outputs of that launch are not valid")
 
 
 def lm_head_accept(h: torch.Tensor, lm_head: torch.Tensor, ids: torch.Tensor | None = None,

@@ -137,15 +137,18 @@ class StackOracle:
         """Greedy M=1 decode of one token (no attention: the next token is a function of this one)."""
         return self.argmax(self.logits(self.forward_stack([tok]), self.final_norm))[0]
 
-    def decode_step(self, cur: int, margins: list | None = None, draft_fn=None):
-        """-> (row [A, d0, d1, bonus], count, next token, n_accept); draft_fn(h, A)
-        replaces the MTP block's drafts when given."""
+    def decode_step(self, cur: int, margins: list | None = None, draft_fn=None, n_draft: int = 2):
+        """-> (row [A, drafts, bonus] ([A] without drafts), count, next token,
+        n_accept); draft_fn(h, A) replaces the MTP block's drafts when given;
+        n_draft = 0 is the reference's plain greedy step (engine.py:2858-2862)."""
         h = self.forward_stack([cur])
         lg = self.logits(h, self.final_norm)
         a = self.argmax(lg)[0]
         if margins is not None:
             margins.append(top2_gap(lg[0]))
-        dr = self.drafts(h, a, 2) if draft_fn is None else list(draft_fn(h, a))
+        if n_draft == 0 and draft_fn is None:
+            return [a], 1, a, 0
+        dr = self.drafts(h, a, n_draft) if draft_fn is None else list(draft_fn(h, a))
         combined = [a] + dr
         lv = self.logits(self.forward_stack(combined), self.final_norm)
         if margins is not None:
@@ -155,14 +158,14 @@ class StackOracle:
         count = 1 + (n_acc + 1 if n_acc > 0 else 0)
         return [a] + dr + [bonus], count, (bonus if n_acc > 0 else a), n_acc
 
-    def generate(self, first: int, steps: int, margins: list | None = None, draft_fn=None):
+    def generate(self, first: int, steps: int, margins: list | None = None, draft_fn=None, n_draft: int = 2):
         """Greedy decode -> (tokens, accepted drafts per step), as the device loop emits them."""
         cur, tokens, accs = first, [], []
         for _ in range(steps):
-            row, count, cur, n_acc = self.decode_step(cur, margins, draft_fn)
+            row, count, cur, n_acc = self.decode_step(cur, margins, draft_fn, n_draft)
             tokens.append(row[0])
             if count > 1:
-                tokens.extend(row[1:count - 1] + [row[3]])
+                tokens.extend(row[1:count - 1] + [row[-1]])
             accs.append(n_acc)
         return tokens, accs
 

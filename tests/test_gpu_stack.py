@@ -183,3 +183,89 @@ def test_graph_replays_equal_eager(model):
     eager = eng.generate_greedy(600, 6, graph=False)
     for _ in range(2):
         assert eng.generate_greedy(600, 6, graph=True) == eager
+
+
+@pytest.mark.parametrize("n_draft", [0, 1, 3])
+def test_draft_counts_match_oracle(model, n_draft):
+    """config.mtp_num_draft = 0 is plain greedy decode (one token a step); 1 and
+    3 drafts verify T = 2 and T = 4 rows.  Eager and graph streams equal the
+    oracle's and the greedy chain; the layer status stays 0."""
+    eng, so = model
+    old = eng.config.mtp_num_draft
+    eng.config.mtp_num_draft = n_draft
+    try:
+        assert eng.draft_count() == n_draft
+        ref = so.generate(77, 4, n_draft=n_draft)
+        for graph in (False, True):
+            assert eng.generate_greedy(77, 4, graph=graph) == ref, graph
+    finally:
+        eng.config.mtp_num_draft = old
+    tokens, accs = ref
+    assert all(0 <= a <= n_draft for a in accs)
+    if n_draft == 0:
+        assert len(tokens) == 4 and accs == [0] * 4
+    assert tokens == chain(77, len(tokens), so.next_token)
+    assert ops.moe_layer_status(eng.device) == 0
+
+
+def test_verify_reads_status_and_accepts(model):
+    """_mtp_verify_batched: greedy acceptance of [A, drafts] against the oracle,
+    bonus logits of the row the acceptance names, status words read at the
+    same sync; no drafts -> (0, None)."""
+    eng, so = model
+    dev = eng.device
+    assert eng._mtp_verify_batched(torch.zeros(1, 0, dtype=torch.int64, device=dev), 0.0) == (0, None)
+    a = so.next_token(123)
+    d0 = so.next_token(a)
+    d1 = so.next_token(d0)
+    for drafts, want in (([d0, d1], 2), ([d0, (d1 + 1) % V], 1), ([(d0 + 1) % V, d1], 0)):
+        main = torch.tensor([[a]], dtype=torch.int64, device=dev)
+        n, bonus = eng._mtp_verify_batched(torch.tensor([drafts], dtype=torch.int64, device=dev), 0.0,
+                                           main_pred_id=main)
+        assert n == want, drafts
+        lv = so.logits(so.forward_stack([a] + drafts), so.final_norm)
+        n_ref, row = orc.mtp_accept(lv, [a] + drafts)
+        assert n_ref == want
+        # the bonus row of the device's own verify logits; its greedy token is the oracle's
+        combined = torch.tensor([[a] + drafts], dtype=torch.int64, device=dev)
+        _, hf = eng._forward_stack(combined)
+        logits, _, _ = ops.lm_head_accept(hf, eng.lm_head, combined.reshape(-1))
+        assert torch.equal(bonus, logits[row:row + 1]), drafts
+        assert so.argmax(np16(bonus)) == so.argmax(lv[row:row + 1])
+
+
+def test_loader_entries_match_oracle(model):
+    """The reference-shaped loaders: _load_expert_weights gives int8 data and
+    fp32 scales equal to the E8M0 values 2^(e-127); _load_bf16_deq and
+    _get_shared_expert give the oracle's dequantisations bit for bit; the FP4
+    FFN from the fp32-scale entry equals the one from the E8M0 bytes."""
+    from home_seek_amd import fused_moe
+    eng, so = model
+    layer, eid = 1, 5
+    ex = so.expert(layer, eid)
+    ent = eng._load_expert_weights(layer, eid)
+    assert [e[2] for e in ent] == ["fp4_gpu"] * 3
+    for (w, s, _), name in zip(ent, ("w1", "w3", "w2")):
+        assert w.dtype == torch.int8 and s.dtype == torch.float32
+        assert np.array_equal(w.view(torch.uint8).cpu().numpy(), ex[name])
+        want = np.ldexp(np.float32(1.0), ex[name + "_scale"].astype(np.int32) - 127).astype(np.float32)
+        assert np.array_equal(s.cpu().numpy(), want), name
+    for t, name in zip(eng._load_bf16_deq(layer, eid), ("w1", "w3", "w2")):
+        assert np.array_equal(np16(t), ex[name + "_bf16"]), name
+    sh = so.shared(layer)
+    for t, name in zip(eng._get_shared_expert(layer), ("w1", "w3", "w2")):
+        assert np.array_equal(np16(t), sh[name + "_bf16"]), name
+    x = torch.from_numpy(orc.bf16_to_f32(so._normal(999, 3 * D, 0.0, 1.0).reshape(3, D))).to(
+        eng.device, torch.bfloat16)
+    (w1, s1, _), (w3, s3, _), (w2, s2, _) = ent
+    raw = eng._load_expert_fp4_raw(layer, eid)
+    y32 = fused_moe.fused_expert_ffn_triton(x, w1, w3, w2, w1_scale=s1, w3_scale=s3, w2_scale=s2)
+    y8 = fused_moe.fused_expert_ffn_triton(x, raw[0], raw[2], raw[4], w1_scale=raw[1], w3_scale=raw[3],
+                                           w2_scale=raw[5])
+    assert torch.equal(y32, y8)
+    ref = orc.expert_ffn_fp32(np16(x), ex["w1_bf16"], ex["w3_bf16"], ex["w2_bf16"], so.limit)
+    # the bf16 output adds its own rounding (half a bf16 step) to the FFN bar
+    y = y32.float().cpu().numpy().astype(np.float64)
+    err = np.abs(y - ref)
+    print(f"[fp4_gpu entry FFN] rel-L2 {np.linalg.norm(y - ref) / np.linalg.norm(ref):.3e}")
+    assert np.all(err <= 2e-2 + np.abs(ref) * 2.0 ** -8)
