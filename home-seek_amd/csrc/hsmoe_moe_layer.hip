@@ -72,6 +72,10 @@ constexpr int kWaitShared = 4610;  //   the shared down's wait for the gate and 
 constexpr int kWaitPart = 4611;    //   a row group's wait for the slots' partials
 constexpr int kMaxRowGroups = 2048;
 constexpr size_t kCtlBytes = 4096;
+// Once a launch's tag reaches kRearmTag its last workgroup zeroes the tagged
+// words and restarts the epoch at 0, so tags never wrap onto words that old
+// launches left in the workspace.
+constexpr unsigned kRearmTag = 1u << 31;
 // Router scores: kScoreCopies copies of [m][n_exp] tagged words, each copy
 // 4 KiB aligned, so that the workgroups polling them spread over many memory
 // channels.
@@ -97,6 +101,9 @@ struct LayerParams {
   uint64_t* act;   // tagged [S][m][i] weighted activations of the routed slots
   uint64_t* sgh;   // tagged [2][m][i] shared expert gate (0) and up (1) row sums
   uint64_t* part;  // tagged [S + 1][m][d] per-slot down partials (slot S: shared)
+  uint4* wipe;      // the workspace after the control words, zeroed at a re-arm
+  int64_t wipe_n;   //   (16-byte units)
+  unsigned* status_out;  // or null: receives this launch's status, the sticky word is cleared
   // item ranges [start, end): R is [0, n_router); the others follow in an
   // order where every item's producers come before it
   int n_router, sgu0, sgu1, sd0, sd1, gu0, gu1, d0, d1, n_items;
@@ -154,6 +161,7 @@ struct Shared {
   int flag;
   int n_routed;
   int have_plan;
+  int last;  // this workgroup is the last of the launch to finish
   alignas(4) unsigned char valid[kMaxExperts];  // expert e has a table entry (plan build)
   alignas(4) unsigned char used[kMaxExperts];   // expert e is selected by some token (plan build)
   short rank[kMaxExperts];                      // slot of a selected expert (plan build)
@@ -759,17 +767,34 @@ __global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
   // that needs the plan (the plan waits only for R items, which wait for
   // nothing)
   if (blockIdx.x == gridDim.x - 1 && !g_sh.have_plan) plan_item(kernarg);
-  // the last workgroup to finish (every workgroup has read the epoch by then)
-  // advances the epoch to this launch's tag and re-arms the counter
+  // the last workgroup to finish (every workgroup has read the epoch and is
+  // done with the workspace by then) advances the epoch to this launch's tag,
+  // or at kRearmTag zeroes the tagged words and restarts the epoch at 0, and
+  // re-arms the counter
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0 && add_agent(p.ctl + kCtlDone, 1u) == gridDim.x - 1) {
-    store_agent(p.ctl + kCtlEpoch, launch_tag(p.ctl));
+  if (threadIdx.x == 0) g_sh.last = add_agent(p.ctl + kCtlDone, 1u) == gridDim.x - 1;
+  __syncthreads();
+  if (!g_sh.last) return;
+  const unsigned tag = launch_tag(p.ctl);
+  if (tag >= kRearmTag) {
+    const uint4 zero = {0u, 0u, 0u, 0u};
+    for (int64_t k = threadIdx.x; k < p.wipe_n; k += kThreads) p.wipe[k] = zero;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (p.status_out) {
+      *p.status_out = load_agent(p.ctl + kCtlErr);
+      store_agent(p.ctl + kCtlErr, 0u);
+    }
+    store_agent(p.ctl + kCtlEpoch, tag >= kRearmTag ? 0u : tag);
     store_agent(p.ctl + kCtlDone, 0u);
   }
 }
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+size_t layer_lds(int64_t m, int64_t d, int64_t i) { return (size_t)(m * d > 2 * m * i ? m * d : 2 * m * i) * 2; }
 int64_t score_stride_words(int64_t m, int64_t n_exp) { return (m * n_exp * 8 + 4095) / 4096 * 512; }
 size_t scores_bytes(int64_t m, int64_t n_exp) { return (size_t)kScoreCopies * score_stride_words(m, n_exp) * 8; }
 size_t act_bytes(int64_t m, int64_t i, int top_k) { return align256((size_t)(m * top_k + 2) * m * i * 8); }
@@ -818,13 +843,13 @@ extern "C" size_t hsmoe_moe_layer_workspace_size(int64_t m, int64_t d, int64_t i
   return kCtlBytes + scores_bytes(m, n_experts) + act_bytes(m, i, top_k) + part_bytes(m, d, top_k);
 }
 
-extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
-                                      const float* gate_bias, int64_t n_experts, int top_k, float routed_scaling,
-                                      const uint64_t* expert_table, int scale_kind, const uint64_t* shared,
-                                      float swiglu_limit, int64_t* topk_idx_out, float* topk_w_out,
-                                      void* logits_out, float* out_f32, void* out_bf16, void* workspace,
-                                      size_t workspace_bytes, hsmoe_stream_t stream) {
-  const char* name = "hsmoe_moe_layer_decode";
+namespace {
+
+// Checks the arguments of a layer launch (not the workspace) -> HSMOE_OK or an error.
+int check_layer_args(const char* name, const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
+                     int64_t n_experts, int top_k, const uint64_t* expert_table, int scale_kind,
+                     const int64_t* topk_idx_out, const float* topk_w_out, const float* out_f32,
+                     const void* out_bf16) {
   if (!x || !gate_w || !expert_table || !topk_idx_out || !topk_w_out || (!out_f32 && !out_bf16))
     return fail(HSMOE_ERR_ARG, "%s: null pointer or no output", name);
   if (scale_kind != HSMOE_SCALE_E8M0 && scale_kind != HSMOE_SCALE_F32)
@@ -838,12 +863,18 @@ extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64
   if (!expert_fits(d, i))
     return fail(HSMOE_ERR_SHAPE, "%s: d*i too large (an expert matrix must stay below 4 GiB)", name);
   if (!aligned(x, 16) || !aligned(gate_w, 16)) return fail(HSMOE_ERR_SHAPE, "%s: x and gate_w must be 16-byte aligned", name);
-  const size_t need = hsmoe_moe_layer_workspace_size(m, d, i, n_experts, top_k);
-  if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
-    return fail(HSMOE_ERR_WORKSPACE, "%s: zero-filled workspace of %zu bytes (256-byte aligned) needed", name, need);
-  const size_t lds = (size_t)(m * d > 2 * m * i ? m * d : 2 * m * i) * 2;
-  if (lds > 65536) return fail(HSMOE_ERR_SHAPE, "%s: m*d and 2*m*i tiles must fit in 64 KiB of LDS", name);
+  if (layer_lds(m, d, i) > 65536) return fail(HSMOE_ERR_SHAPE, "%s: m*d and 2*m*i tiles must fit in 64 KiB of LDS", name);
+  return HSMOE_OK;
+}
 
+// Launches moe_layer_kernel on checked arguments and a workspace of
+// workspace_bytes >= hsmoe_moe_layer_workspace_size bytes (256-byte aligned).
+int launch_layer(const char* name, const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
+                 const float* gate_bias, int64_t n_experts, int top_k, float routed_scaling,
+                 const uint64_t* expert_table, int scale_kind, const uint64_t* shared, float swiglu_limit,
+                 int64_t* topk_idx_out, float* topk_w_out, void* logits_out, float* out_f32, void* out_bf16,
+                 void* workspace, size_t workspace_bytes, unsigned* status_out, hipStream_t stream) {
+  const size_t lds = layer_lds(m, d, i);
   LayerParams p;
   p.x = (const uint16_t*)x;
   p.gate_w = (const uint16_t*)gate_w;
@@ -874,6 +905,9 @@ extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64
   p.sgh = p.act + (size_t)p.S * m * i;
   ws += act_bytes(m, i, top_k);
   p.part = (uint64_t*)ws;
+  p.wipe = (uint4*)((char*)workspace + kCtlBytes);
+  p.wipe_n = (int64_t)((workspace_bytes - kCtlBytes) / 16);
+  p.status_out = status_out;
   const int has_shared = shared ? 1 : 0;
   p.n_router = (int)n_experts;
   // Item order after R (producers always before their consumers): SGU, SD,
@@ -906,8 +940,28 @@ extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64
   int rc = resident_workgroups(lds, &resident);
   if (rc) return rc;
   const int grid = resident < p.n_items ? resident : p.n_items;
-  hipLaunchKernelGGL(moe_layer_kernel, dim3((unsigned)grid), dim3(kThreads), lds, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(moe_layer_kernel, dim3((unsigned)grid), dim3(kThreads), lds, stream, p);
   return check_launch(name);
+}
+
+}  // namespace
+
+extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
+                                      const float* gate_bias, int64_t n_experts, int top_k, float routed_scaling,
+                                      const uint64_t* expert_table, int scale_kind, const uint64_t* shared,
+                                      float swiglu_limit, int64_t* topk_idx_out, float* topk_w_out,
+                                      void* logits_out, float* out_f32, void* out_bf16, void* workspace,
+                                      size_t workspace_bytes, hsmoe_stream_t stream) {
+  const char* name = "hsmoe_moe_layer_decode";
+  int rc = check_layer_args(name, x, m, d, i, gate_w, n_experts, top_k, expert_table, scale_kind, topk_idx_out,
+                            topk_w_out, out_f32, out_bf16);
+  if (rc) return rc;
+  const size_t need = hsmoe_moe_layer_workspace_size(m, d, i, n_experts, top_k);
+  if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+    return fail(HSMOE_ERR_WORKSPACE, "%s: zero-filled workspace of %zu bytes (256-byte aligned) needed", name, need);
+  return launch_layer(name, x, m, d, i, gate_w, gate_bias, n_experts, top_k, routed_scaling, expert_table,
+                      scale_kind, shared, swiglu_limit, topk_idx_out, topk_w_out, logits_out, out_f32, out_bf16,
+                      workspace, workspace_bytes, nullptr, (hipStream_t)stream);
 }
 
 extern "C" size_t hsmoe_moe_layer_status_offset(void) { return (size_t)kCtlErr * 4; }

@@ -22,23 +22,20 @@ MAX_DECODE_TOKENS = 8
 MAX_LAYER_EXPERTS = 256  # expert count the one-launch layer kernel handles
 
 _workspaces: dict[tuple, torch.Tensor] = {}
-_layer_launches: dict[tuple, int] = {}  # eager layer launches per workspace since it was zeroed
-
-# The layer kernel tags every cross-workgroup word with its launch number (a
-# 32-bit epoch kept in the workspace), so a workspace must be zeroed again
-# before 2^32 launches; it is re-armed (zeroed once its epoch passes 2^31) by
-# moe_layer_status, which reads the epoch, and every _REARM_CHECK_EVERY eager
-# launches.  Graph replays are not counted: a replay loop reads the status
-# (GreedyDecoder.result does) at least once per 2^31 launches.
-_REARM_EPOCH = 1 << 31
-_REARM_CHECK_EVERY = 1 << 24
 
 
 def _workspace(device: torch.device, purpose: str, nbytes: int) -> torch.Tensor:
+    """Zero-filled device workspace of at least nbytes, one per (device,
+    stream, purpose), grown when a call needs more.  A grown layer workspace
+    keeps the sticky status word of the one it replaces."""
     key = (device.index, stream_ptr(device), purpose)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        new = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        if ws is not None and purpose == "layer":
+            off = lib().hsmoe_moe_layer_status_offset()
+            new[off:off + 4].copy_(ws[off:off + 4])
+        ws = new
         _workspaces[key] = ws
     return ws
 
@@ -267,11 +264,6 @@ def moe_layer_decode(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Ten
     logits = torch.empty(m, n_exp, dtype=torch.bfloat16, device=dev) if want_logits else None
     nbytes = lib().hsmoe_moe_layer_workspace_size(m, d, i, n_exp, top_k)
     ws = _workspace(dev, "layer", nbytes)
-    key = (dev.index, stream_ptr(dev), "layer")
-    n = _layer_launches.get(key, 0) + 1
-    _layer_launches[key] = n
-    if n % _REARM_CHECK_EVERY == 0 and not torch.cuda.is_current_stream_capturing():
-        _rearm_if_old(ws)
     rc = lib().hsmoe_moe_layer_decode(ptr(x), m, d, i, ptr(gate_w), ptr(gate_bias), n_exp, top_k, scaling,
                                       ptr(table), scale_kind, ptr(shared), swiglu_limit, ptr(idx_out), ptr(w_out),
                                       ptr(logits), ptr(out_f32), ptr(out_bf16), ptr(ws), ws.numel(),
@@ -295,28 +287,15 @@ def moe_layer_status_words(device: torch.device | None = None, stream: int | Non
     return [ws[off:off + 4].view(torch.int32) for ws in _layer_workspaces(device, stream)]
 
 
-def _rearm_if_old(ws: torch.Tensor) -> None:
-    """Zeroes a layer workspace whose epoch passed 2^31 (synchronises the device)."""
-    epoch = int(ws[0:4].view(torch.int32).item()) & 0xFFFFFFFF
-    if epoch >= _REARM_EPOCH:
-        torch.cuda.synchronize(ws.device)
-        ws.zero_()
-
-
 def moe_layer_status(device: torch.device | None = None, stream: int | None = None) -> int:
     """The layer kernel's sticky status word: 0 when every cross-workgroup wait
     of every launch completed, else 1 + the code of a wait that gave up (the
     outputs of that launch are not valid).  Reads the workspaces of `stream`,
-    or of every stream of the device when None, and re-arms a workspace whose
-    launch epoch is old.  Synchronises the device."""
+    or of every stream of the device when None.  Synchronises the device."""
     device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
-    words = moe_layer_status_words(device, stream)
     status = 0
-    for w in words:
+    for w in moe_layer_status_words(device, stream):
         status = status or int(w.item())
-    if not torch.cuda.is_current_stream_capturing():
-        for ws in _layer_workspaces(device, stream):
-            _rearm_if_old(ws)
     return status
 
 

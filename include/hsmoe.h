@@ -149,8 +149,13 @@ int hsmoe_moe_down(const void* x_dev, int64_t m, int64_t d, int64_t i, const int
  * [m, top_k] receive the routing; logits_out bf16 [m, n_experts] or NULL;
  * out_f32 / out_bf16 as in hsmoe_moe_decode.
  * m in [1, 8], d % 512 == 0, d <= 8192, i % 512 == 0, n_experts <= 256,
- * top_k <= 16 (larger expert counts: hsmoe_router_topk + hsmoe_moe_decode).  The workgroups hand work to each other through the workspace;
- * the launch never has more workgroups than the device holds at once.  The
+ * top_k <= 16 (larger expert counts: hsmoe_router_topk + hsmoe_moe_decode).
+ * The workgroups hand work to each other through the workspace, with words
+ * tagged by a launch number kept in the workspace; the launch never has more
+ * workgroups than the device holds at once.  The workspace is zero-filled
+ * once, before its first launch; launches on one stream then need nothing
+ * between them, whatever their shapes (every 2^31 launches the last
+ * workgroup zeroes the whole workspace and the numbering restarts).  The
  * uint32 at byte hsmoe_moe_layer_status_offset() of the workspace stays 0
  * unless a cross-workgroup wait gave up (then the outputs are not valid).
  */

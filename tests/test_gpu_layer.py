@@ -187,3 +187,27 @@ def test_fused_layer_rejects_bad_shapes(layer, dev):
     x = synthetic.hidden(SEED, 400, 9, D, dev)
     with pytest.raises(ValueError):
         ops.moe_layer_decode(x, gate, bias, store.table(0), ops.SCALE_E8M0, None, I)
+
+
+def test_workspace_rearms_before_the_tags_wrap(layer, dev):
+    """The launch whose tag reaches 2^31 zeroes the workspace after the control
+    words and restarts the epoch at 0 (so tags never wrap onto old words);
+    results stay bit-identical across it.  The epoch is set from the host to
+    just below the re-arm point."""
+    store, gate, bias = layer
+    x = synthetic.hidden(SEED, 700, 3, D, dev)
+    ref = staged(x, gate, bias, store.table(0), store.shared_entry(0))
+    fused(x, gate, bias, store.table(0), store.shared_entry(0))
+    (ws,) = ops._layer_workspaces(dev, ops.stream_ptr(dev))
+    epoch = ws[0:4].view(torch.int32)
+    epoch.fill_(0x7FFFFFFE)
+    ctl = 4096
+    for want_epoch in (0x7FFFFFFF, 0, 1):
+        a = fused(x, gate, bias, store.table(0), store.shared_entry(0))
+        torch.cuda.synchronize()
+        assert int(epoch.item()) & 0xFFFFFFFF == want_epoch
+        if want_epoch == 0:
+            assert int(torch.count_nonzero(ws[ctl:])) == 0
+        for got, r, what in zip(a, ref, ("bf16", "f32", "idx", "w")):
+            assert torch.equal(got, r), (want_epoch, what)
+    assert ops.moe_layer_status(dev) == 0
