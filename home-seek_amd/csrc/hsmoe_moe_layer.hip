@@ -944,6 +944,11 @@ int launch_layer(const char* name, const void* x, int64_t m, int64_t d, int64_t 
   return check_launch(name);
 }
 
+__global__ void __launch_bounds__(256) clear_kernel(uint4* __restrict__ p, int64_t n) {
+  const uint4 zero = {0u, 0u, 0u, 0u};
+  for (int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x; k < n; k += (int64_t)gridDim.x * 256) p[k] = zero;
+}
+
 }  // namespace
 
 extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
@@ -962,6 +967,67 @@ extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64
   return launch_layer(name, x, m, d, i, gate_w, gate_bias, n_experts, top_k, routed_scaling, expert_table,
                       scale_kind, shared, swiglu_limit, topk_idx_out, topk_w_out, logits_out, out_f32, out_bf16,
                       workspace, workspace_bytes, nullptr, (hipStream_t)stream);
+}
+
+// Scratch of hsmoe_moe_layer_decode_noalloc: the workspace of every call of
+// that entry point on one GPU.  Each GPU the library runs on holds its own
+// copy, at its own address, until the process ends; it starts zeroed (static
+// storage) and every launch leaves it ready for the next one.  In host code
+// `scratch` names a host-side stand-in, not device memory: host code uses only
+// the address hipGetSymbolAddress gives for the current device (g_scratch).
+static __device__ __align__(256) unsigned char scratch[HSMOE_LAYER_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, looked up once per device (with the
+// device current) and cleared on `stream` at that first call.
+int device_scratch(const char* name, hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(HSMOE_ERR_LAUNCH, "%s: no current device (or device index >= %d)", name, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(HSMOE_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name, dev,
+                  hipGetErrorString(e));
+    const int64_t n = (int64_t)(HSMOE_LAYER_SCRATCH_BYTES / 16);
+    hipLaunchKernelGGL(clear_kernel, dim3(1024), dim3(256), 0, stream, (uint4*)ptr, n);
+    const int rc = check_launch(name);
+    if (rc) return rc;
+    g_scratch[dev] = ptr;
+  }
+  *out = g_scratch[dev];
+  return HSMOE_OK;
+}
+}  // namespace
+
+extern "C" int hsmoe_moe_layer_decode_noalloc(const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
+                                              const float* gate_bias, int64_t n_experts, int top_k,
+                                              float routed_scaling, const uint64_t* expert_table, int scale_kind,
+                                              const uint64_t* shared, float swiglu_limit, int64_t* topk_idx_out,
+                                              float* topk_w_out, void* logits_out, float* out_f32, void* out_bf16,
+                                              uint32_t* status_out, hsmoe_stream_t stream) {
+  const char* name = "hsmoe_moe_layer_decode_noalloc";
+  int rc = check_layer_args(name, x, m, d, i, gate_w, n_experts, top_k, expert_table, scale_kind, topk_idx_out,
+                            topk_w_out, out_f32, out_bf16);
+  if (rc) return rc;
+  if (!status_out || !aligned(status_out, 4)) return fail(HSMOE_ERR_ARG, "%s: status_out must be a device uint32", name);
+  const size_t need = hsmoe_moe_layer_workspace_size(m, d, i, n_experts, top_k);
+  if (need > HSMOE_LAYER_SCRATCH_BYTES)
+    return fail(HSMOE_ERR_WORKSPACE,
+                "%s: this shape needs %zu bytes of scratch, more than the %zu the library holds per GPU "
+                "(use hsmoe_moe_layer_decode with a workspace)", name, need, (size_t)HSMOE_LAYER_SCRATCH_BYTES);
+  void* ws = nullptr;
+  rc = device_scratch(name, (hipStream_t)stream, &ws);
+  if (rc) return rc;
+  return launch_layer(name, x, m, d, i, gate_w, gate_bias, n_experts, top_k, routed_scaling, expert_table,
+                      scale_kind, shared, swiglu_limit, topk_idx_out, topk_w_out, logits_out, out_f32, out_bf16, ws,
+                      HSMOE_LAYER_SCRATCH_BYTES, (unsigned*)status_out, (hipStream_t)stream);
 }
 
 extern "C" size_t hsmoe_moe_layer_status_offset(void) { return (size_t)kCtlErr * 4; }

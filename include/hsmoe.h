@@ -6,7 +6,9 @@
  *     allocates, frees or copies user memory.  Scratch memory comes from a
  *     caller-provided `workspace` of at least the size the matching
  *     *_workspace_size() call returns, zero-filled once when it is allocated
- *     (kernels leave their counters at zero when they finish).
+ *     (kernels leave their counters at zero when they finish); the one
+ *     exception, hsmoe_moe_layer_decode_noalloc, uses a static scratch array
+ *     of the library instead.
  *   - bf16 tensors are passed as raw 16-bit storage, row-major, contiguous
  *     unless a row stride argument says otherwise.
  *   - All work is enqueued on `stream` (a hipStream_t; NULL is the default
@@ -167,6 +169,30 @@ int hsmoe_moe_layer_decode(const void* x_dev, int64_t m, int64_t d, int64_t i, c
                            void* logits_out_dev, float* out_f32_dev, void* out_bf16_dev, void* workspace_dev,
                            size_t workspace_bytes, hsmoe_stream_t stream);
 size_t hsmoe_moe_layer_status_offset(void);
+
+/* hsmoe_moe_layer_decode without a workspace and without any allocation.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Arguments and results are those of
+ * hsmoe_moe_layer_decode, bit for bit, with the library's own scratch in
+ * place of the workspace: a static device array of HSMOE_LAYER_SCRATCH_BYTES
+ * per GPU, held from the library's load until the process ends.  Shapes whose
+ * hsmoe_moe_layer_workspace_size exceeds it are rejected with
+ * HSMOE_ERR_WORKSPACE (8 MiB holds m <= 5 at d = 4096, i = 2048, 256 experts,
+ * top-6).  status_out: device uint32 that receives 0, or 1 + the code of a
+ * cross-workgroup wait that gave up in this launch (its outputs are then not
+ * valid).  Every call on one GPU shares that GPU's scratch: calls that overlap
+ * on one GPU (other streams, other threads) race and must be serialised by the
+ * caller; consecutive calls on one stream need nothing between them.  The
+ * first call on a device looks up its scratch and clears it on `stream`.
+ */
+#define HSMOE_LAYER_SCRATCH_BYTES ((size_t)8 << 20)
+int hsmoe_moe_layer_decode_noalloc(const void* x_dev, int64_t m, int64_t d, int64_t i, const void* gate_w_dev,
+                                   const float* gate_bias_dev, int64_t n_experts, int top_k, float routed_scaling,
+                                   const uint64_t* expert_table_dev, int scale_kind, const uint64_t* shared_dev,
+                                   float swiglu_limit, int64_t* topk_idx_out_dev, float* topk_w_out_dev,
+                                   void* logits_out_dev, float* out_f32_dev, void* out_bf16_dev,
+                                   uint32_t* status_out_dev, hsmoe_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Routed-expert SwiGLU FFN for many tokens (prefill, m > 8): a grouped GEMM
