@@ -11,9 +11,10 @@ follows.  bf16 tensors are numpy uint16 arrays of raw bf16 bits.
 Parity pins (tests/test_oracle_*.py): the reference's own KATs (stable top-k,
 E8M0 127/128/126, dequant interleave / per-group scale, SiLU-not-sigmoid,
 scaling-factor sum, MTP accept/reject cases), torch's own casts for every
-format conversion, splitmix64's published outputs, and brute-force / closed
-forms on small inputs.  Functions without such a pin are marked
-"parity unpinned" in their docstring.
+format conversion, torch's own bf16 ops running the reference's FFN and
+router formulas on inputs whose sums are exact, float64 evaluations,
+splitmix64's published outputs, and brute-force / closed forms on small
+inputs.  Every function is pinned by at least one of them.
 """
 from __future__ import annotations
 
@@ -291,15 +292,19 @@ def expert_ffn_fp32(x: np.ndarray, w1: np.ndarray, w3: np.ndarray, w2: np.ndarra
 
 
 def expert_ffn_ref_bf16(x: np.ndarray, w1: np.ndarray, w3: np.ndarray, w2: np.ndarray,
-                        limit: float = 10.0) -> np.ndarray:
-    """fused_expert_ffn_pt exactly as the reference's M<=8 route rounds: gate/up
-    bf16, activation bf16, fp32-accumulated down -> fp32 before the final bf16 store.
-    (parity unpinned against the reference's BLAS accumulation order)"""
+                        limit: float = 10.0, steps: bool = False):
+    """fused_expert_ffn_pt (fused_moe.py:383-395) with the reference's bf16
+    rounding points: gate/up bf16 (`hidden @ w1.t()`), activation bf16
+    (`.to(w1.dtype)`), fp32-accumulated down -> fp32 before the final bf16 store.
+    steps=True -> dict of the bf16 bits of gate, up, act and the fp32 out.
+    Pinned by torch's own bf16 ops on inputs whose gate/up sums are exact:
+    gate/up bit-exact, act and out within one bf16 step."""
     xf = bf16_to_f32(x)
-    gate = bf16_to_f32(f32_to_bf16(xf @ bf16_to_f32(w1).T))
-    up = bf16_to_f32(f32_to_bf16(xf @ bf16_to_f32(w3).T))
-    act = bf16_to_f32(f32_to_bf16(_swiglu_f32(gate, up, limit)))
-    return (act @ bf16_to_f32(w2).T).astype(np.float32)
+    gate = f32_to_bf16(xf @ bf16_to_f32(w1).T)
+    up = f32_to_bf16(xf @ bf16_to_f32(w3).T)
+    act = f32_to_bf16(_swiglu_f32(bf16_to_f32(gate), bf16_to_f32(up), limit))
+    out = (bf16_to_f32(act) @ bf16_to_f32(w2).T).astype(np.float32)
+    return {"gate": gate, "up": up, "act": act, "out": out} if steps else out
 
 
 def moe_layer_fp32(x: np.ndarray, idx: np.ndarray, w: np.ndarray, experts: dict, shared: dict | None,
@@ -324,12 +329,15 @@ def moe_layer_fp32(x: np.ndarray, idx: np.ndarray, w: np.ndarray, experts: dict,
 
 
 def moe_layer_reference(x: np.ndarray, idx: np.ndarray, w: np.ndarray, experts: dict, shared: dict | None,
-                        limit: float = 10.0) -> np.ndarray:
+                        limit: float = 10.0, steps: bool = False):
     """The reference's T>1 union route (_forward_legacy torch branch, fused_moe.py:458-551)
     plus the bf16 shared add (engine.py:1530-1536), with all its bf16 roundings:
     bf16 gate/up, bf16 activation, bf16 routing weights, bf16 act*ew product,
-    one fp32-accumulated down GEMM over the union, bf16 output; returns bf16 bits.
-    (parity unpinned against the reference's BLAS accumulation order)"""
+    fp32-accumulated down over the union, bf16 output; returns bf16 bits
+    (steps=True -> dict with the bf16 routing weights "ew" [m, n_union], the
+    union "union", the routed sum "routed", the shared output "shared" and "out").
+    Pinned by torch's own ops on exact-sum inputs: ew bit-exact, routed and
+    out within one bf16 step, the shared add bit-exact."""
     m, d = x.shape
     union = sorted({int(e) for e in idx.reshape(-1) if int(e) >= 0 and int(e) in experts})
     xf = bf16_to_f32(x)
@@ -349,10 +357,18 @@ def moe_layer_reference(x: np.ndarray, idx: np.ndarray, w: np.ndarray, experts: 
         weighted = bf16_to_f32(f32_to_bf16((act * ew[:, q:q + 1]).astype(np.float32)))
         acc = (acc + weighted @ bf16_to_f32(ex["w2_bf16"]).T).astype(np.float32)
     routed = f32_to_bf16(acc)
-    if shared is None:
-        return routed
-    sh = f32_to_bf16(expert_ffn_ref_bf16(x, shared["w1_bf16"], shared["w3_bf16"], shared["w2_bf16"], limit))
-    return f32_to_bf16(bf16_to_f32(routed) + bf16_to_f32(sh))
+    sh, out = None, routed
+    if shared is not None:
+        sh = f32_to_bf16(expert_ffn_ref_bf16(x, shared["w1_bf16"], shared["w3_bf16"], shared["w2_bf16"], limit))
+        out = bf16_add_bits(routed, sh)
+    if steps:
+        return {"ew": f32_to_bf16(ew), "union": union, "routed": routed, "shared": sh, "out": out}
+    return out
+
+
+def bf16_add_bits(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """torch's bf16 + bf16: the two values added in fp32, the sum rounded to bf16."""
+    return f32_to_bf16((bf16_to_f32(a) + bf16_to_f32(b)).astype(np.float32))
 
 
 def rms_norm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:

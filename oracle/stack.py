@@ -20,9 +20,10 @@ bf16 tensors are uint16 arrays of raw bits; a bf16 + bf16 sum is the fp32 sum
 rounded once (torch's bf16 add).  The MoE FFN is fp32-accumulated and rounded
 to bf16 once, which the device matches within the FFN tolerance, not bit for
 bit: per-layer comparisons use that tolerance, and token streams agree where
-the argmax margins exceed the propagated error.  The composition itself is
-parity unpinned against the reference's generate(), which cannot run here
-(no attention state, no checkpoint); its pieces are pinned individually.
+the argmax margins exceed the propagated error.  The pieces are pinned
+individually; the decode loop's emission rule (decode_step + generate) is
+pinned against a direct restatement of the reference loop (engine.py:2809-2922
+at temperature 0) on a toy model whose next token is known, for 0-3 drafts.
 """
 from __future__ import annotations
 
