@@ -316,3 +316,56 @@ def test_softplus_matches_torch_across_its_threshold():
     got = orc.softplus_f32(x)
     np.testing.assert_allclose(got, ref, rtol=4e-7, atol=1e-30)  # libm exp/log1p: within 3 ulp
     assert np.array_equal(got[x > 20], x[x > 20])
+
+
+def test_cpu_ref_route_matches_oracle():
+    """oracle/cpu_ref.py (the timed CPU baseline: the reference's torch route)
+    against the numpy/C oracle: FP4 and FP8 dequant bit for bit, router ids
+    and weights, the union route + shared add within one bf16 step of
+    moe_layer_reference, and the greedy acceptance."""
+    from oracle import cpu_ref
+    rng = np.random.default_rng(31)
+    n, k = 64, 256
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    e8 = rng.integers(119, 125, (n, k // 32), dtype=np.uint8)
+    got = cpu_ref.dequant_fp4(torch.from_numpy(packed), torch.from_numpy(e8))
+    assert np.array_equal(torch_bits(got), orc.dequant_fp4(packed, e8))
+    q = orc.gen_e4m3(orc.key(3, 1), 256 * 384).reshape(256, 384)
+    sc = rng.uniform(0.5, 2.0, (2, 3)).astype(np.float32) / 448
+    got8 = cpu_ref.dequant_fp8(torch.from_numpy(q), torch.from_numpy(sc))
+    assert np.array_equal(torch_bits(got8), orc.dequant_fp8(q, sc))
+    # router on exact-sum inputs
+    x, _ = exact_sum_inputs(rng, 3, 64, 8)
+    gate = (rng.integers(-15, 16, (32, 64)) / 16.0).astype(np.float32)
+    bias = (rng.integers(-16, 17, 32) / 64.0).astype(np.float32)
+    idx, w = cpu_ref.router(bf16t(x), bf16t(gate), torch.from_numpy(bias), 6, 1.5)
+    ridx, rw = orc.router(orc.f32_to_bf16(x), orc.f32_to_bf16(gate), bias, 6, 1.5)
+    assert np.array_equal(idx.numpy(), ridx)
+    np.testing.assert_allclose(w.numpy(), rw, rtol=1e-6)
+    # union route + shared on FP4 experts (per-call dequant inside cpu_ref)
+    d, i, n_exp = 128, 128, 6  # one 128 x 128 scale block per shared matrix
+    xb = orc.f32_to_bf16(rng.integers(-6, 7, (3, d)).astype(np.float32))
+    raw, experts = {}, {}
+    for e in range(n_exp):
+        mats = [(rng.integers(0, 256, (i, d // 2), dtype=np.uint8), rng.integers(119, 125, (i, d // 32), dtype=np.uint8)),
+                (rng.integers(0, 256, (i, d // 2), dtype=np.uint8), rng.integers(119, 125, (i, d // 32), dtype=np.uint8)),
+                (rng.integers(0, 256, (d, i // 2), dtype=np.uint8), rng.integers(119, 125, (d, i // 32), dtype=np.uint8))]
+        raw[e] = tuple(torch.from_numpy(t) for pair in mats for t in pair)
+        experts[e] = {nm: orc.dequant_fp4(p, s) for nm, (p, s) in zip(("w1_bf16", "w3_bf16", "w2_bf16"), mats)}
+    sq = [orc.gen_e4m3(orc.key(4, j), 128 * 128).reshape(128, 128) for j in range(3)]
+    ss = [np.array([[rng.uniform(0.5, 2.0) / 448]], dtype=np.float32) for _ in range(3)]
+    shared_raw = (torch.from_numpy(sq[0]), torch.from_numpy(ss[0]), torch.from_numpy(sq[1]), torch.from_numpy(ss[1]),
+                  torch.from_numpy(sq[2]), torch.from_numpy(ss[2]))
+    shared = {nm: orc.dequant_fp8(q_, s_) for nm, q_, s_ in zip(("w1_bf16", "w3_bf16", "w2_bf16"), sq, ss)}
+    tid = np.array([[0, 2, 5], [1, 2, -1], [4, 3, 0]], dtype=np.int64)
+    tw = rng.uniform(0.1, 1.0, (3, 3)).astype(np.float32)
+    xt = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16)
+    y = cpu_ref.moe_ffn(xt, torch.from_numpy(tid), torch.from_numpy(tw), raw.get, shared_raw)
+    ref = orc.moe_layer_reference(xb, tid, tw, experts, shared, LIMIT)
+    assert bf16_steps_apart(torch_bits(y), ref).max() <= 1
+    # acceptance
+    lg = np.zeros((3, 10), dtype=np.float32)
+    lg[0, 4], lg[1, 7], lg[2, 1] = 1, 1, 1
+    for cid, want in (([9, 4, 7], (2, 2)), ([9, 4, 6], (1, 1)), ([9, 5, 7], (0, 0))):
+        _, n_acc, row = cpu_ref.lm_head_accept(torch.eye(3, dtype=torch.bfloat16), bf16t(lg.T.copy()), cid)
+        assert (n_acc, row) == want == orc.mtp_accept(orc.f32_to_bf16(lg), cid)
