@@ -332,30 +332,32 @@ def run_headline(torch, args, lb: LayerBench, cpu_info):
 # ---------------------------------------------------------------- config 0
 
 def run_config0(torch, args, lb: LayerBench, cpu_info):
-    """One routed FP4 expert at M=1: hsmoe_moe_decode with a single id, 32
-    (layer, expert) pairs rotated (428 MB)."""
+    """One routed FP4 expert at M=1: the layer kernel with one given id and no
+    shared expert (hsmoe_moe_layer_decode_routed), 32 (layer, expert) pairs
+    rotated (428 MB)."""
     from home_seek_amd import ops, synthetic
     dev = lb.dev
     pairs = [(l, (37 * j + 11 * l) % E) for l in range(lb.L) for j in range(32 // lb.L)]
     xs = [synthetic.hidden(args.seed, 4000 + j, 1, D, dev) for j in range(len(pairs))]
     idx = [torch.tensor([[e]], dtype=torch.int64, device=dev) for _, e in pairs]
-    one = torch.ones(1, 1, dtype=torch.float32, device=dev)
     outs = [torch.empty(1, D, dtype=torch.bfloat16, device=dev) for _ in pairs]
 
     def launch(j):
         l, _ = pairs[j]
-        ops.moe_decode(xs[j], idx[j], one, lb.tables[l], ops.SCALE_E8M0, None, 10.0, out_bf16=outs[j], d=D, i=I)
+        ops.moe_layer_decode_routed(xs[j], idx[j], lb.tables[l], ops.SCALE_E8M0, None, I, weight_all=1.0, top_k=1,
+                                    out_bf16=outs[j])
 
     steps = 8 * len(pairs)
     total_ms, samples = timed_launches(torch, lb.stream, launch, len(pairs), steps, len(pairs))
+    ops.check_moe_layer_status(dev)
     sp = spread(samples)
     us = sp["median_us"]
     gbs = EXPERT_BYTES / (us * 1e-6) / 1e9
     res = {"workload": "config 0: one routed FP4 expert (dequant + SwiGLU FFN), M=1, D=4096 I=2048",
            "value": round(gbs, 1), "unit": "GB/s", "steps": steps, "ms_per_step": round(us * 1e-3, 5),
            "timing": sp, "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-           "roofline": roofline("moe_gate_up_kernel + moe_down_kernel (one expert, two launches)",
-                                EXPERT_BYTES + 2 * D * 2, us), "cpu_baseline": None}
+           "roofline": roofline("moe_layer_kernel with one given id (one launch)", EXPERT_BYTES + 2 * D * 2, us),
+           "cpu_baseline": None}
     if not args.no_cpu_baseline:
         from oracle import cpu_ref
         l, e = pairs[0]

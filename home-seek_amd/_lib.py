@@ -45,6 +45,9 @@ _SIGNATURES = {
                                       _int, _c_void_p, _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                       _c_void_p, _size, _c_void_p]),
     "hsmoe_moe_layer_status_offset": (_size, []),
+    "hsmoe_moe_layer_decode_routed": (_int, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _f32,
+                                             _int, _c_void_p, _i64, _int, _c_void_p, _f32, _c_void_p, _c_void_p,
+                                             _c_void_p, _size, _c_void_p]),
     "hsmoe_moe_layer_decode_noalloc": (_int, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _i64, _int, _f32,
                                               _c_void_p, _int, _c_void_p, _f32, _c_void_p, _c_void_p, _c_void_p,
                                               _c_void_p, _c_void_p, _c_void_p, _c_void_p]),

@@ -104,6 +104,14 @@ struct LayerParams {
   uint4* wipe;      // the workspace after the control words, zeroed at a re-arm
   int64_t wipe_n;   //   (16-byte units)
   unsigned* status_out;  // or null: receives this launch's status, the sticky word is cleared
+  // given routing (no router items) when route_idx is set: token t's ids are
+  // route_idx[route_tok[t]][:] (a token table of route_rows rows) or, without
+  // route_tok, route_idx[t][:]; its weights route_w[t][:] or all route_wconst
+  const int64_t* route_idx;
+  const int64_t* route_tok;
+  const float* route_w;
+  float route_wconst;
+  int64_t route_rows;
   // item ranges [start, end): R is [0, n_router); the others follow in an
   // order where every item's producers come before it
   int n_router, sgu0, sgu1, sd0, sd1, gu0, gu1, d0, d1, n_items;
@@ -167,16 +175,11 @@ struct Shared {
   short rank[kMaxExperts];                      // slot of a selected expert (plan build)
 };
 
-// The slot plan of this launch in LDS (n_exp <= kThreads): thread e holds
-// expert e's table entry.  Wave w takes the top-k of tokens w, w + kWaves, ...
-// (ties to the lower index) from the token's tagged scores, polled with
-// agent-scope loads until all carry this launch's tag; then the distinct
-// valid expert ids in ascending order become the slots, each token's weight
-// for a slot being its top-k weight for that id (a token's ids are distinct:
-// at most one), else 0 -- the union of _forward_legacy, fused_moe.py:466-476.
-__device__ __forceinline__ void build_plan(const LayerParams& p, Shared& sh, const uint64_t (&my_ent)[6]) {
+// The router part of the slot plan: wave w takes the top-k of tokens w,
+// w + kWaves (ties to the lower index) from the tokens' tagged scores, polled
+// with agent-scope loads until all carry this launch's tag.
+__device__ __forceinline__ void build_plan_scores(const LayerParams& p, Shared& sh, const uint64_t (&my_ent)[6]) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int n = p.m * p.top_k;
   // wave w holds tokens w and w + kWaves (m <= 2 * kWaves), 4 scores per lane
   // each (n_exp <= 256); a lane reloads only the words it has not yet seen
   static_assert(kMaxTok <= 2 * kWaves, "two tokens per wave");
@@ -230,6 +233,13 @@ __device__ __forceinline__ void build_plan(const LayerParams& p, Shared& sh, con
     const int t = wave + kWaves * j;
     if (t < p.m) wave_topk_vals<4>(v[j], p.n_exp, p.top_k, p.scaling, sh.idx + t * p.top_k, sh.w + t * p.top_k);
   }
+}
+
+// Slots from sh.idx / sh.w: the distinct valid ids ascending, each token's
+// weight of each slot, the slots' table entries.
+__device__ __forceinline__ void finish_plan(const LayerParams& p, Shared& sh, const uint64_t (&my_ent)[6]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = p.m * p.top_k;
   __syncthreads();
   // Wave 0 alone (LDS accesses of one wave take effect in program order):
   // mark the selected valid experts, rank them ascending (lane l counts
@@ -261,9 +271,24 @@ __device__ __forceinline__ void build_plan(const LayerParams& p, Shared& sh, con
       if (sl < base && t < p.m) sh.wt[sl][t] = 0.0f;
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    for (int j = lane; j < n; j += 64) {
-      const int64_t e = sh.idx[j];
-      if (e >= 0 && e < p.n_exp && sh.valid[e]) sh.wt[sh.rank[e]][j / p.top_k] = __fadd_rn(0.0f, sh.w[j]);
+    if (!p.route_idx) {  // router ids: distinct per token
+      for (int j = lane; j < n; j += 64) {
+        const int64_t e = sh.idx[j];
+        if (e >= 0 && e < p.n_exp && sh.valid[e]) sh.wt[sh.rank[e]][j / p.top_k] = __fadd_rn(0.0f, sh.w[j]);
+      }
+    } else {  // given ids may repeat within a token: their weights add, in k order
+      for (int j = lane; j < n; j += 64) {
+        const int64_t e = sh.idx[j];
+        const int t = j / p.top_k, c0 = t * p.top_k;
+        bool first = e >= 0 && e < p.n_exp && sh.valid[e];
+        for (int c = c0; c < j && first; ++c) first = sh.idx[c] != e;
+        if (first) {
+          float w = 0.0f;
+          for (int c = c0; c < c0 + p.top_k; ++c)
+            if (sh.idx[c] == e) w = __fadd_rn(w, sh.w[c]);
+          sh.wt[sh.rank[e]][t] = w;
+        }
+      }
     }
     if (lane == 0) sh.n_routed = base;
   }
@@ -278,12 +303,44 @@ __device__ __forceinline__ void build_plan(const LayerParams& p, Shared& sh, con
   __syncthreads();
 }
 
+// The slot plan of this launch in LDS (n_exp <= kThreads): thread e holds
+// expert e's table entry.  The ids and weights come from the router's scores
+// (build_plan_scores) or, with given routing, from the caller's arrays (a
+// hash layer's token table, engine.py:1018-1023); then the distinct valid
+// expert ids in ascending order become the slots, each token's weight for a
+// slot being its weight for that id (a token's ids are distinct: at most
+// one), else 0 -- the union of _forward_legacy, fused_moe.py:466-476.
+__device__ __forceinline__ void build_plan(const LayerParams& p, Shared& sh, const uint64_t (&my_ent)[6]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = p.m * p.top_k;
+  if (p.route_idx) {
+    // given routing: nothing to wait for (ids of tokens outside the table: -1)
+    for (int j = threadIdx.x; j < n; j += kThreads) {
+      const int t = j / p.top_k, c = j - t * p.top_k;
+      int64_t e = -1;
+      if (p.route_tok) {
+        const int64_t tok = ldg<int64_t>(p.route_tok + t);
+        if (tok >= 0 && tok < p.route_rows) e = ldg<int64_t>(p.route_idx + tok * p.top_k + c);
+      } else {
+        e = ldg<int64_t>(p.route_idx + j);
+      }
+      sh.idx[j] = e;
+      sh.w[j] = p.route_w ? ldg<float>(p.route_w + j) : p.route_wconst;
+    }
+    if ((int)threadIdx.x < p.n_exp) sh.valid[threadIdx.x] = my_ent[0] != 0ull;
+    sh.used[threadIdx.x] = 0;
+  } else {
+    build_plan_scores(p, sh, my_ent);
+  }
+  finish_plan(p, sh, my_ent);
+}
+
 // The routing outputs (and the zero output of a layer with no valid expert
 // and no shared expert), written once by the plan builder.
 __device__ __forceinline__ void write_routing(const LayerParams& p, Shared& sh) {
   for (int j = threadIdx.x; j < p.m * p.top_k; j += kThreads) {
-    p.idx_out[j] = sh.idx[j];
-    p.w_out[j] = sh.w[j];
+    if (p.idx_out) p.idx_out[j] = sh.idx[j];
+    if (p.w_out) p.w_out[j] = sh.w[j];
   }
   if (sh.n_routed == 0 && !p.shared) {
     // no down item will run, and the output is zero (_forward_legacy returns
@@ -849,8 +906,8 @@ namespace {
 int check_layer_args(const char* name, const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
                      int64_t n_experts, int top_k, const uint64_t* expert_table, int scale_kind,
                      const int64_t* topk_idx_out, const float* topk_w_out, const float* out_f32,
-                     const void* out_bf16) {
-  if (!x || !gate_w || !expert_table || !topk_idx_out || !topk_w_out || (!out_f32 && !out_bf16))
+                     const void* out_bf16, bool given_route = false) {
+  if (!x || !expert_table || (!out_f32 && !out_bf16) || (!given_route && (!gate_w || !topk_idx_out || !topk_w_out)))
     return fail(HSMOE_ERR_ARG, "%s: null pointer or no output", name);
   if (scale_kind != HSMOE_SCALE_E8M0 && scale_kind != HSMOE_SCALE_F32)
     return fail(HSMOE_ERR_ARG, "%s: unknown scale_kind %d", name, scale_kind);
@@ -862,20 +919,35 @@ int check_layer_args(const char* name, const void* x, int64_t m, int64_t d, int6
                 (long long)d, (long long)i);
   if (!expert_fits(d, i))
     return fail(HSMOE_ERR_SHAPE, "%s: d*i too large (an expert matrix must stay below 4 GiB)", name);
-  if (!aligned(x, 16) || !aligned(gate_w, 16)) return fail(HSMOE_ERR_SHAPE, "%s: x and gate_w must be 16-byte aligned", name);
+  if (!aligned(x, 16) || (!given_route && !aligned(gate_w, 16)))
+    return fail(HSMOE_ERR_SHAPE, "%s: x and gate_w must be 16-byte aligned", name);
   if (layer_lds(m, d, i) > 65536) return fail(HSMOE_ERR_SHAPE, "%s: m*d and 2*m*i tiles must fit in 64 KiB of LDS", name);
   return HSMOE_OK;
 }
 
 // Launches moe_layer_kernel on checked arguments and a workspace of
 // workspace_bytes >= hsmoe_moe_layer_workspace_size bytes (256-byte aligned).
+struct GivenRoute {
+  const int64_t* idx;
+  const int64_t* tok;
+  int64_t rows;
+  const float* w;
+  float wconst;
+};
+
 int launch_layer(const char* name, const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
                  const float* gate_bias, int64_t n_experts, int top_k, float routed_scaling,
                  const uint64_t* expert_table, int scale_kind, const uint64_t* shared, float swiglu_limit,
                  int64_t* topk_idx_out, float* topk_w_out, void* logits_out, float* out_f32, void* out_bf16,
-                 void* workspace, size_t workspace_bytes, unsigned* status_out, hipStream_t stream) {
+                 void* workspace, size_t workspace_bytes, unsigned* status_out, hipStream_t stream,
+                 const GivenRoute* route = nullptr) {
   const size_t lds = layer_lds(m, d, i);
   LayerParams p;
+  p.route_idx = route ? route->idx : nullptr;
+  p.route_tok = route ? route->tok : nullptr;
+  p.route_rows = route ? route->rows : 0;
+  p.route_w = route ? route->w : nullptr;
+  p.route_wconst = route ? route->wconst : 0.0f;
   p.x = (const uint16_t*)x;
   p.gate_w = (const uint16_t*)gate_w;
   p.bias = gate_bias;
@@ -909,7 +981,7 @@ int launch_layer(const char* name, const void* x, int64_t m, int64_t d, int64_t 
   p.wipe_n = (int64_t)((workspace_bytes - kCtlBytes) / 16);
   p.status_out = status_out;
   const int has_shared = shared ? 1 : 0;
-  p.n_router = (int)n_experts;
+  p.n_router = route ? 0 : (int)n_experts;
   // Item order after R (producers always before their consumers): SGU, SD,
   // GU, D -- the shared down streams while the routed work is still waiting
   // for the plan; for m <= 2 SGU, GU, D, SD -- there the routed work starts
@@ -967,6 +1039,27 @@ extern "C" int hsmoe_moe_layer_decode(const void* x, int64_t m, int64_t d, int64
   return launch_layer(name, x, m, d, i, gate_w, gate_bias, n_experts, top_k, routed_scaling, expert_table,
                       scale_kind, shared, swiglu_limit, topk_idx_out, topk_w_out, logits_out, out_f32, out_bf16,
                       workspace, workspace_bytes, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int hsmoe_moe_layer_decode_routed(const void* x, int64_t m, int64_t d, int64_t i, const int64_t* topk_idx,
+                                             const int64_t* token_ids, int64_t table_rows, const float* topk_w,
+                                             float weight_all, int top_k, const uint64_t* expert_table,
+                                             int64_t n_experts, int scale_kind, const uint64_t* shared,
+                                             float swiglu_limit, float* out_f32, void* out_bf16, void* workspace,
+                                             size_t workspace_bytes, hsmoe_stream_t stream) {
+  const char* name = "hsmoe_moe_layer_decode_routed";
+  if (!topk_idx) return fail(HSMOE_ERR_ARG, "%s: null topk_idx", name);
+  if (token_ids && table_rows < 1) return fail(HSMOE_ERR_ARG, "%s: a token table needs table_rows >= 1", name);
+  int rc = check_layer_args(name, x, m, d, i, nullptr, n_experts, top_k, expert_table, scale_kind, nullptr, nullptr,
+                            out_f32, out_bf16, true);
+  if (rc) return rc;
+  const size_t need = hsmoe_moe_layer_workspace_size(m, d, i, n_experts, top_k);
+  if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+    return fail(HSMOE_ERR_WORKSPACE, "%s: zero-filled workspace of %zu bytes (256-byte aligned) needed", name, need);
+  const GivenRoute route{topk_idx, token_ids, token_ids ? table_rows : 0, topk_w, weight_all};
+  return launch_layer(name, x, m, d, i, nullptr, nullptr, n_experts, top_k, 1.0f, expert_table, scale_kind, shared,
+                      swiglu_limit, nullptr, nullptr, nullptr, out_f32, out_bf16, workspace, workspace_bytes, nullptr,
+                      (hipStream_t)stream, &route);
 }
 
 // Scratch of hsmoe_moe_layer_decode_noalloc: the workspace of every call of

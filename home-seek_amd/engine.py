@@ -66,6 +66,20 @@ class HomeSeekMoEEngine:
     def _get_layer_weights(self, layer_idx: int) -> dict:
         return self._layer_weights[layer_idx]
 
+    @property
+    def _last_routed_idx(self):
+        """Expert ids [B*T, k] of the last _forward_ffn; a hash layer's are looked
+        up (tid2eid[input_ids]) only when read, outside the decode hot path."""
+        r = self._last_route
+        if isinstance(r, tuple):
+            table, ids = r
+            return table[ids]
+        return r
+
+    @_last_routed_idx.setter
+    def _last_routed_idx(self, value):
+        self._last_route = value
+
     def _load_expert_fp4_raw(self, layer_idx: int, eid: int):
         """(w1, w1_scale, w3, w3_scale, w2, w2_scale) device views (E8M0 scales), or None."""
         try:
@@ -144,15 +158,30 @@ class HomeSeekMoEEngine:
                 out_bf16=torch.empty(B * T, D, dtype=torch.bfloat16, device=flat.device))
             self._last_routed_idx = idx
             return out.reshape(B, T, D).to(hidden_states.dtype), set()
+        k = self.config.num_experts_per_tok
+        table = self.store.table(layer_idx)
+        if (hashed and B * T <= ops.MAX_DECODE_TOKENS and table.shape[0] <= ops.MAX_LAYER_EXPERTS
+                and flat.dtype == torch.bfloat16 and tid2eid.dtype == torch.int64 and tid2eid.is_contiguous()
+                and tid2eid.device == flat.device and input_ids.device == flat.device
+                and input_ids.dtype == torch.int64):
+            # hash ids (tid2eid[input_ids], weight 1/k, engine.py:1018-1023) looked up
+            # inside the one-launch layer kernel (hsmoe_moe_layer_decode_routed)
+            ids = input_ids.reshape(-1)
+            out, _ = ops.moe_layer_decode_routed(
+                flat, tid2eid, table, SCALE_E8M0, self.store.shared_entry(layer_idx),
+                self.config.moe_intermediate_size, weight_all=1.0 / k, token_ids=ids, top_k=k,
+                swiglu_limit=self.config.swiglu_limit, out_f32=out_f32,
+                out_bf16=torch.empty(B * T, D, dtype=torch.bfloat16, device=flat.device))
+            self._last_routed_idx = (tid2eid, ids)
+            return out.reshape(B, T, D).to(hidden_states.dtype), set()
         if hashed:
             idx, w = self._compute_hash_experts(input_ids.to(hidden_states.device), layer_idx, tid2eid)
         else:
             idx, w = self._compute_routing_experts(flat, gate_w, gate_bias)
-        k = self.config.num_experts_per_tok
         idx = idx.reshape(B * T, k)
         w = w.reshape(B * T, k)
         self._last_routed_idx = idx
-        out = self._fused_moe.forward_table(flat, idx, w, self.store.table(layer_idx), SCALE_E8M0,
+        out = self._fused_moe.forward_table(flat, idx, w, table, SCALE_E8M0,
                                             self.store.shared_entry(layer_idx), out_f32=out_f32)
         return out.reshape(B, T, D).to(hidden_states.dtype), set()
 

@@ -63,11 +63,24 @@ def _run_decode_chunks(x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Te
         ops.moe_prefill(x, topk_idx, topk_w, table, scale_kind, shared, limit, out_bf16=out, out_f32=out_f32, i=i)
         return out
     step = ops.MAX_DECODE_TOKENS
+    k = topk_idx.shape[-1]
     for a in range(0, m, step):
         b = min(m, a + step)
-        ops.moe_decode(x[a:b], topk_idx[a:b], topk_w[a:b], table, scale_kind, shared, limit,
-                       out_bf16=out[a:b], out_f32=None if out_f32 is None else out_f32[a:b], d=d, i=i)
+        o32 = None if out_f32 is None else out_f32[a:b]
+        if _layer_kernel_fits(b - a, d, i, table.shape[0], k):
+            # one persistent launch (hsmoe_moe_layer_decode_routed), bit-identical to moe_decode
+            ops.moe_layer_decode_routed(x[a:b], topk_idx[a:b], table, scale_kind, shared, i, topk_w=topk_w[a:b],
+                                        top_k=k, swiglu_limit=limit, out_bf16=out[a:b], out_f32=o32)
+        else:
+            ops.moe_decode(x[a:b], topk_idx[a:b], topk_w[a:b], table, scale_kind, shared, limit,
+                           out_bf16=out[a:b], out_f32=o32, d=d, i=i)
     return out
+
+
+def _layer_kernel_fits(m: int, d: int, i: int, n_experts: int, top_k: int) -> bool:
+    """The shapes the one-launch layer kernel takes (else the two-launch decode kernels)."""
+    return (m <= ops.MAX_DECODE_TOKENS and n_experts <= ops.MAX_LAYER_EXPERTS and top_k <= 16 and d % 512 == 0
+            and i % 512 == 0 and d <= 8192 and max(m * d, 2 * m * i) * 2 <= 65536)
 
 
 class FusedMoEFFN:

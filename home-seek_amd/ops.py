@@ -14,7 +14,7 @@ from ._lib import SCALE_E8M0, SCALE_F32, check, lib, ptr, require_cuda, stream_p
 
 __all__ = [
     "SCALE_E8M0", "SCALE_F32", "scale_kind_of", "fp4_dequant_bf16", "fp8_dequant_bf16", "router_topk",
-    "moe_decode", "moe_layer_decode", "moe_layer_status", "moe_layer_status_words", "lm_head_accept", "expert_table",
+    "moe_decode", "moe_layer_decode", "moe_layer_decode_routed", "moe_layer_status", "moe_layer_status_words", "lm_head_accept", "expert_table",
     "shared_entry", "MAX_DECODE_TOKENS", "MAX_LAYER_EXPERTS",
 ]
 
@@ -271,6 +271,54 @@ def moe_layer_decode(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Ten
     check(rc, "hsmoe_moe_layer_decode")
     res = (out_bf16, out_f32, idx_out, w_out)
     return res + (logits,) if want_logits else res
+
+
+def moe_layer_decode_routed(x: torch.Tensor, topk_idx: torch.Tensor, table: torch.Tensor, scale_kind: int,
+                            shared: torch.Tensor | None, i: int, topk_w: torch.Tensor | None = None,
+                            weight_all: float = 1.0, token_ids: torch.Tensor | None = None, top_k: int | None = None,
+                            swiglu_limit: float = 10.0, out_bf16: torch.Tensor | None = None,
+                            out_f32: torch.Tensor | None = None):
+    """Routed + shared experts of M <= 8 tokens in one launch with the routing
+    given (hsmoe_moe_layer_decode_routed); returns (out_bf16, out_f32).
+
+    token_ids None: topk_idx [M, k] are the ids.  Otherwise topk_idx is a
+    token table [V, k] (a hash layer's tid2eid) and token t's ids are row
+    token_ids[t].  topk_w [M, k] or None (every weight weight_all).  Same
+    results as moe_decode on the same ids and weights.  Inside a graph capture
+    the inputs must already be contiguous device tensors of the right dtypes."""
+    dev = require_cuda(x, topk_idx, table, shared, topk_w, token_ids)
+    if x.dtype != torch.bfloat16:
+        raise TypeError("hidden states must be bf16")
+    x = x.contiguous()
+    m, d = x.shape
+    if m > MAX_DECODE_TOKENS:
+        raise ValueError(f"moe_layer_decode_routed handles at most {MAX_DECODE_TOKENS} tokens, got {m}")
+    topk_idx = topk_idx.to(torch.int64).contiguous()
+    k = topk_idx.shape[-1] if top_k is None else top_k
+    rows = 0
+    if token_ids is not None:
+        token_ids = token_ids.reshape(-1).to(torch.int64).contiguous()
+        if token_ids.numel() != m:
+            raise ValueError("token_ids must hold one id per token")
+        rows = topk_idx.shape[0]
+        if topk_idx.dim() != 2 or topk_idx.shape[1] != k:
+            raise ValueError("a token table must be [V, top_k]")
+    elif topk_idx.numel() != m * k:
+        raise ValueError("topk_idx must be [M, top_k]")
+    if topk_w is not None:
+        topk_w = topk_w.to(torch.float32).contiguous()
+        if topk_w.numel() != m * k:
+            raise ValueError("topk_w must be [M, top_k]")
+    if out_bf16 is None and out_f32 is None:
+        out_bf16 = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
+    n_exp = table.shape[0]
+    ws = _workspace(dev, "layer", lib().hsmoe_moe_layer_workspace_size(m, d, i, n_exp, k))
+    rc = lib().hsmoe_moe_layer_decode_routed(ptr(x), m, d, i, ptr(topk_idx), ptr(token_ids), rows, ptr(topk_w),
+                                             float(weight_all), k, ptr(table), n_exp, scale_kind, ptr(shared),
+                                             swiglu_limit, ptr(out_f32), ptr(out_bf16), ptr(ws), ws.numel(),
+                                             stream_ptr(dev))
+    check(rc, "hsmoe_moe_layer_decode_routed")
+    return out_bf16, out_f32
 
 
 def _layer_workspaces(device: torch.device, stream: int | None = None) -> list[torch.Tensor]:

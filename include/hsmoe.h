@@ -170,6 +170,30 @@ int hsmoe_moe_layer_decode(const void* x_dev, int64_t m, int64_t d, int64_t i, c
                            size_t workspace_bytes, hsmoe_stream_t stream);
 size_t hsmoe_moe_layer_status_offset(void);
 
+/* The same one-launch layer with the routing given instead of computed:
+ * routed + shared experts of m <= 8 tokens in one persistent launch.
+ * Replaces _forward_ffn on the hash-routed layers (reference
+ * src/home_seek/inference_engine/engine.py:1425-1428, _compute_hash_experts
+ * engine.py:1018-1023: ids tid2eid[input_ids], every weight 1/k) and
+ * FusedMoEFFN.forward with caller-given top-k (src/home_seek/fused_moe.py:
+ * 447-563) + the shared-expert add (engine.py:1530-1536), bit-identical to
+ * hsmoe_moe_decode on the same ids and weights.
+ * token_ids_dev == NULL: topk_idx_dev is int64 [m, top_k].  Otherwise
+ * topk_idx_dev is a token table int64 [table_rows, top_k] and token t's ids
+ * are row token_ids_dev[t] (a token id outside [0, table_rows) selects no
+ * expert).  topk_w_dev: fp32 [m, top_k], or NULL: every weight is weight_all.
+ * Ids < 0 or >= n_experts and absent table entries are skipped; an id given
+ * twice for one token has its weights added (in k order), as in
+ * hsmoe_moe_decode.  Workspace, status word, shapes and outputs as in
+ * hsmoe_moe_layer_decode (hsmoe_moe_layer_workspace_size).
+ */
+int hsmoe_moe_layer_decode_routed(const void* x_dev, int64_t m, int64_t d, int64_t i, const int64_t* topk_idx_dev,
+                                  const int64_t* token_ids_dev, int64_t table_rows, const float* topk_w_dev,
+                                  float weight_all, int top_k, const uint64_t* expert_table_dev, int64_t n_experts,
+                                  int scale_kind, const uint64_t* shared_dev, float swiglu_limit, float* out_f32_dev,
+                                  void* out_bf16_dev, void* workspace_dev, size_t workspace_bytes,
+                                  hsmoe_stream_t stream);
+
 /* hsmoe_moe_layer_decode without a workspace and without any allocation.
  * No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

@@ -211,3 +211,59 @@ def test_workspace_rearms_before_the_tags_wrap(layer, dev):
         for got, r, what in zip(a, ref, ("bf16", "f32", "idx", "w")):
             assert torch.equal(got, r), (want_epoch, what)
     assert ops.moe_layer_status(dev) == 0
+
+
+def routed(x, idx, table, shared, w=None, weight_all=1.0, token_ids=None, k=K):
+    f32 = torch.empty(x.shape[0], D, dtype=torch.float32, device=x.device)
+    bf = torch.empty(x.shape[0], D, dtype=torch.bfloat16, device=x.device)
+    out, _ = ops.moe_layer_decode_routed(x, idx, table, ops.SCALE_E8M0, shared, I, topk_w=w, weight_all=weight_all,
+                                         token_ids=token_ids, top_k=k, out_f32=f32, out_bf16=bf)
+    return out, f32
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_routed_layer_equals_staged_decode(layer, dev, m):
+    """Given ids and weights (FusedMoEFFN.forward's contract): bit-identical to
+    moe_decode, with an invalid id, an out-of-range id and, for m = 3, an id
+    given twice for one token (its weights add, in k order)."""
+    store, gate, bias = layer
+    x = synthetic.hidden(SEED, 800 + m, m, D, dev)
+    idx, w = ops.router_topk(x, gate, bias, K, 1.5)
+    idx = idx.clone()
+    idx[0, 1] = -1
+    idx[-1, 2] = E + 5
+    if m == 3:
+        idx[1, 4] = idx[1, 0]
+    a = routed(x, idx, store.table(0), store.shared_entry(0), w=w)
+    f32 = torch.empty(m, D, dtype=torch.float32, device=dev)
+    b = ops.moe_decode(x, idx, w, store.table(0), ops.SCALE_E8M0, store.shared_entry(0), 10.0, out_f32=f32, d=D, i=I)
+    torch.cuda.synchronize()
+    assert ops.moe_layer_status(dev) == 0
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], f32)
+
+
+def test_routed_layer_token_table_is_hash_routing(layer, dev):
+    """A token table (a hash layer's tid2eid): ids tid2eid[token], every weight
+    1/k, a token id outside the table selects nothing; equals moe_decode on the
+    looked-up ids; also one expert alone with no shared expert (one id, weight 1)."""
+    store, _, _ = layer
+    V = 1000
+    g = torch.Generator().manual_seed(5)
+    tid2eid = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(V)]).to(dev)
+    tok = torch.tensor([7, 999, 123, V + 3], dtype=torch.int64, device=dev)
+    x = synthetic.hidden(SEED, 900, 4, D, dev)
+    a = routed(x, tid2eid, store.table(0), store.shared_entry(0), weight_all=1.0 / K, token_ids=tok)
+    ids = tid2eid[tok.clamp(max=V - 1)].clone()
+    ids[3] = -1
+    w = torch.full((4, K), 1.0 / K, dtype=torch.float32, device=dev)
+    f32 = torch.empty(4, D, dtype=torch.float32, device=dev)
+    ops.moe_decode(x, ids, w, store.table(0), ops.SCALE_E8M0, store.shared_entry(0), 10.0, out_f32=f32, d=D, i=I)
+    torch.cuda.synchronize()
+    assert torch.equal(a[1], f32)
+    one = routed(x[:1], torch.tensor([[17]], device=dev), store.table(0), None, k=1)
+    f1 = torch.empty(1, D, dtype=torch.float32, device=dev)
+    ops.moe_decode(x[:1], torch.tensor([[17]], device=dev), torch.ones(1, 1, device=dev), store.table(0),
+                   ops.SCALE_E8M0, None, 10.0, out_f32=f1, d=D, i=I)
+    torch.cuda.synchronize()
+    assert torch.equal(one[1], f1)
+    assert ops.moe_layer_status(dev) == 0
