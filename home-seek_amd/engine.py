@@ -82,10 +82,9 @@ class HomeSeekMoEEngine:
 
     def _load_expert_fp4_raw(self, layer_idx: int, eid: int):
         """(w1, w1_scale, w3, w3_scale, w2, w2_scale) device views (E8M0 scales), or None."""
-        try:
-            return self.store.expert_views(layer_idx, eid)
-        except IndexError:
+        if not self.store.has_expert(layer_idx, eid):
             return None
+        return self.store.expert_views(layer_idx, eid)
 
     def _load_expert_weights(self, layer_idx: int, eid: int):
         """((w1, s1, fmt), (w3, s3, fmt), (w2, s2, fmt)) with fmt "fp4_gpu" (engine.py:1084-1129).
@@ -116,9 +115,9 @@ class HomeSeekMoEEngine:
 
     def _get_shared_expert(self, layer_idx: int):
         """BF16 (w1, w3, w2) of the FP8 shared expert (load_fp8_weight, weight_loader.py:22-32)."""
-        views = self.store.shared_views(layer_idx)
-        if views is None:
+        if not self.store.has_shared(layer_idx):
             return None
+        views = self.store.shared_views(layer_idx)
         w1, s1, w3, s3, w2, s2 = views
         return ops.fp8_dequant_bf16(w1, s1), ops.fp8_dequant_bf16(w3, s3), ops.fp8_dequant_bf16(w2, s2)
 

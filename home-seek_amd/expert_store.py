@@ -66,6 +66,26 @@ class HbmExpertStore:
         self.buf = torch.empty(total, dtype=torch.uint8, device=self.device)
         self._tables: dict[int, torch.Tensor] = {}
         self._shared_entries: dict[int, torch.Tensor] = {}
+        self._absent: set[tuple[int, int]] = set()  # experts a checkpoint does not hold
+        self._no_shared: set[int] = set()           # layers without a shared expert
+
+    # ------------------------------------------------------------ presence
+    def mark_absent(self, layer: int, eid: int) -> None:
+        """The expert is not in the checkpoint: its table row becomes zero (the
+        kernels skip it, as the reference skips a loader returning None)."""
+        self._expert_base(layer, eid)
+        self._absent.add((layer, eid))
+        self._tables.pop(layer, None)
+
+    def has_expert(self, layer: int, eid: int) -> bool:
+        return 0 <= layer < self.n_layers and 0 <= eid < self.n_experts and (layer, eid) not in self._absent
+
+    def mark_no_shared(self, layer: int) -> None:
+        self._no_shared.add(layer)
+        self._shared_entries.pop(layer, None)
+
+    def has_shared(self, layer: int) -> bool:
+        return self.with_shared and layer not in self._no_shared
 
     # ------------------------------------------------------------ views
     def _expert_base(self, layer: int, eid: int) -> int:
@@ -103,13 +123,16 @@ class HbmExpertStore:
             rows = []
             for e in range(self.n_experts):
                 b = base + e * self.expert_bytes
-                rows.append([b + self._off[n] for n in ("w1", "s1", "w3", "s3", "w2", "s2")])
+                if (layer, e) in self._absent:
+                    rows.append([0] * 6)
+                else:
+                    rows.append([b + self._off[n] for n in ("w1", "s1", "w3", "s3", "w2", "s2")])
             t = torch.tensor(rows, dtype=torch.int64).to(self.device)
             self._tables[layer] = t
         return t
 
     def shared_entry(self, layer: int) -> torch.Tensor | None:
-        if not self.with_shared:
+        if not self.has_shared(layer):
             return None
         t = self._shared_entries.get(layer)
         if t is None:

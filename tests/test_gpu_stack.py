@@ -269,3 +269,42 @@ def test_loader_entries_match_oracle(model):
     err = np.abs(y - ref)
     print(f"[fp4_gpu entry FFN] rel-L2 {np.linalg.norm(y - ref) / np.linalg.norm(ref):.3e}")
     assert np.all(err <= 2e-2 + np.abs(ref) * 2.0 ** -8)
+
+
+def test_checkpoint_round_trip_through_the_loader(model, tmp_path):
+    """The small stack written as a safetensors checkpoint in the reference's
+    key layout and loaded back with home_seek_amd.checkpoint: every layer's
+    FFN (hash layer included) and the MTP block's give the same outputs, bit
+    for bit."""
+    from safetensors.torch import save_file
+    from home_seek_amd import checkpoint
+    eng, _ = model
+    t = {}
+    for l in range(NL + 1):
+        base = f"layers.{l}.ffn" if l < NL else "mtp.0.ffn"
+        for e in range(E):
+            for key, v in zip(checkpoint.expert_keys(f"{base}.experts.{e}"), eng.store.expert_views(l, e)):
+                t[key] = v.cpu()
+        for key, v in zip(checkpoint.expert_keys(f"{base}.shared_experts"), eng.store.shared_views(l)):
+            t[key] = v.cpu()
+        lw = eng._get_layer_weights(l) if l < NL else eng._mtp_weights["layer"]
+        pre = f"layers.{l}" if l < NL else "mtp.0"
+        for short in ("ffn.gate.weight", "ffn.gate.bias", "ffn.gate.tid2eid", "ffn_norm.weight"):
+            if short in lw:
+                t[f"{pre}.{short}"] = lw[short].cpu()
+    for n in ("enorm", "hnorm", "norm"):
+        t[f"mtp.0.{n}.weight"] = eng._mtp_weights[f"{n}.weight"].cpu()
+    t["embed.weight"] = eng.embed.cpu()
+    t["norm.weight"] = eng.norm_weight.cpu()
+    save_file({k: v.contiguous() for k, v in t.items()}, str(tmp_path / "model.safetensors"))
+    eng2 = checkpoint.load_engine(str(tmp_path), config=eng.config, device=eng.device)
+    assert torch.equal(eng2.lm_head, eng.lm_head) and eng2._mtp_weights["layer_idx"] == NL
+    ids = torch.tensor([[3, 900, 17]], dtype=torch.int64, device=eng.device)
+    hn = torch.randn(1, 3, D, device=eng.device).to(torch.bfloat16)
+    for l in range(NL + 1):
+        lw = eng._get_layer_weights(l) if l < NL else eng._mtp_weights["layer"]
+        lw2 = eng2._get_layer_weights(l) if l < NL else eng2._mtp_weights["layer"]
+        a, _ = eng._forward_ffn(hn, lw, l, ids)
+        b, _ = eng2._forward_ffn(hn, lw2, l, ids)
+        assert torch.equal(a, b), l
+    assert ops.moe_layer_status(eng.device) == 0
