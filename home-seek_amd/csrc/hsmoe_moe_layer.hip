@@ -663,7 +663,9 @@ __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg
     // the shared slot's are the SwiGLU of its published gate and up sums
     // (weight 1)
     const int n = m * i;
-    constexpr int kStageWords = 4;  // per thread and round (registers: the W2 batch is live)
+    // per thread and round (registers: the W2 batch is live; the shared slot
+    // reads two planes per word)
+    constexpr int kStageWords = kShared ? 4 : 8;
     for (int u0 = 0; u0 < n; u0 += kStageWords * kThreads) {  // this thread's words u0 + threadIdx.x + kThreads * j
       const int c0 = u0 + (int)threadIdx.x;
       unsigned need = 0;
@@ -778,7 +780,7 @@ __device__ __noinline__ void down_finish(uint64_t kernarg, int q_arg) {
   }
 }
 
-__global__ void __launch_bounds__(kThreads) moe_layer_kernel(LayerParams p) {
+__global__ void __launch_bounds__(kThreads, 2) moe_layer_kernel(LayerParams p) {
   int state = 0;  // 1 while the LDS tile holds x
   if (threadIdx.x == 0) g_sh.have_plan = 0;
   if (p.shared && threadIdx.x < 6) g_sh.ent[p.S][threadIdx.x] = ldg<uint64_t>(p.shared + threadIdx.x);

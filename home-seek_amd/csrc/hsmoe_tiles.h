@@ -175,6 +175,18 @@ __device__ __forceinline__ bf16x8 lds_frag(const uint16_t* tile, int kcols, int 
   return *reinterpret_cast<const bf16x8*>(tile + c * kcols + st * 128 + g * 32 + 8 * j);
 }
 
+// The four B fragments (j = 0..3) of step st, as lds_frag.  The MFMA loops
+// read step st + 1's fragments before multiplying step st, so the LDS latency
+// of one step hides behind the previous step's MFMAs instead of stalling
+// every MFMA on its own read.
+struct Frags {
+  bf16x8 f[4];
+  __device__ __forceinline__ void read(const uint16_t* tile, int kcols, int c, int g, int st, int ncol) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f[j] = lds_frag(tile, kcols, c, g, st, j, ncol);
+  }
+};
+
 // ------------------------------------------------------------ gate / up
 // One wave: rows r0..r0+15 of W1 and W3 ([i][d]) of the slot `ent` over steps
 // [st0, st1) against the m token rows of x ([m][d] bf16 in LDS).  The MFMA
@@ -281,12 +293,18 @@ __device__ __forceinline__ void down_rows(const uint64_t* ent, const uint16_t* a
   Batch<F, kB> bw;
   bw.load(w2, row, i, 0, g);
   ready();
+  Frags ac;
+  ac.read(as, i, r, g, 0, 2 * m);
   for (int st = 0; st < n; st += kB) {
     if (st) bw.load(w2, row, i, st, g);
 #pragma unroll
-    for (int b = 0; b < kB; ++b)
+    for (int b = 0; b < kB; ++b) {
+      Frags an;
+      an.read(as, i, r, g, min(st + b + 1, n - 1), 2 * m);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc = mfma16x16x32(bw.frag(b, j, g), lds_frag(as, i, r, g, st + b, j, 2 * m), acc);
+      for (int j = 0; j < 4; ++j) acc = mfma16x16x32(bw.frag(b, j, g), ac.f[j], acc);
+      ac = an;
+    }
   }
 }
 
