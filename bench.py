@@ -59,9 +59,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="default 800 (headline) / 64 (stack) / 50 (prefill)")
     ap.add_argument("--warmup", type=int, default=None, help="default 40 (headline) / 4 (stack) / 5 (prefill)")
-    ap.add_argument("--workload", choices=("all", "layer", "stack", "prefill"), default="all",
+    ap.add_argument("--workload", choices=("all", "layer", "verify", "stack", "prefill"), default="all",
                     help="all: the headline layer line with configs 0, 2, 3, 4 under 'configs'; "
-                         "layer: the headline only; stack / prefill: that workload as the line")
+                         "layer: the headline only; verify / stack / prefill: config 2 / 4 / 3 as the line")
     ap.add_argument("--configs", default="0,2,3,4", help="sub-workloads of --workload all")
     ap.add_argument("--stack-layers", type=int, default=43)
     ap.add_argument("--stack-steps", type=int, default=16, help="decode steps of config 4 under --workload all")
@@ -697,17 +697,23 @@ def main():
     __graft_entry__.package()
     torch.cuda.set_device(0)
     cpu_info = cpu_setup() if not args.no_cpu_baseline else {"threads": 0}
-    if args.workload in ("stack", "prefill"):
-        fn = run_stack if args.workload == "stack" else run_prefill
-        res = fn(torch, args, cpu_info)
+    if args.workload in ("verify", "stack", "prefill"):
+        if args.workload == "verify":
+            res = run_config2(torch, args, LayerBench(torch, args), cpu_info)
+            res["warmup"] = args.layers
+        else:
+            fn = run_stack if args.workload == "stack" else run_prefill
+            res = fn(torch, args, cpu_info)
         wl = res.pop("workload")
         line = {"metric": METRIC, "value": res.pop("value"), "unit": res.pop("unit"), "n_gpus": 1,
                 "steps": res.pop("steps"), "warmup": res.pop("warmup"), "ms_per_step": res.pop("ms_per_step"),
                 "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": DTYPE,
                 "data": "synthetic (seeded on device)",
-                "config": {"workload": wl, "global_batch": 512 if args.workload == "prefill" else 1,
-                           "seq_len": 512 if args.workload == "prefill" else 1, "parallelism": "none (1 GPU)"}}
+                "config": {"workload": wl, "global_batch": {"prefill": 512, "verify": 3}.get(args.workload, 1),
+                           "seq_len": {"prefill": 512, "verify": 3}.get(args.workload, 1),
+                           "parallelism": "none (1 GPU)"}}
         line.update(res)
+        calib_copy(torch, args)
         print(json.dumps(line))
         return
 
@@ -733,13 +739,19 @@ def main():
             print("[bench] config 4", file=sys.stderr, flush=True)
             configs["4"] = run_stack(torch, args, cpu_info, steps=args.stack_steps, warmup=2)
         line["configs"] = configs
+    calib_copy(torch, args)
+    print(json.dumps(line))
+
+
+def calib_copy(torch, args):
+    """--calib-copy: three copies of a 256 MiB buffer (known bytes) that scale
+    the PMC byte counters of the same run."""
     if args.calib_copy:
         src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-    print(json.dumps(line))
 
 
 if __name__ == "__main__":

@@ -97,7 +97,7 @@ def test_router_ties_and_no_bias(dev):
     assert torch.allclose(w, torch.full_like(w, 0.25))
 
 
-@pytest.mark.parametrize("n_tok,vocab", [(1, 4096), (3, 129280), (8, 1000)])
+@pytest.mark.parametrize("n_tok,vocab", [(1, 4096), (3, 129280), (8, 1000), (2, 70001), (4, 33333)])
 def test_lm_head_logits_argmax_bit_exact(dev, n_tok, vocab):
     seed = 7 + n_tok
     d = 4096 if vocab > 5000 else 512
