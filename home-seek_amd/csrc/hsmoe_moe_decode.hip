@@ -189,10 +189,21 @@ __global__ void __launch_bounds__(64 * kP2Waves) moe_down_kernel(DecodeParams p)
   f32x4 acc = {0, 0, 0, 0};
   // the W2 rows do not depend on the activations: their first batch is in
   // flight while the tile is staged
-  down_slot(slot_format(p.scale_fmt, ent, is_shared), ent, as, p.m, p.i, p.d, r0, acc, [&]() {
+  auto stage = [&]() {
     for (int q = threadIdx.x; q < n16; q += blockDim.x) reinterpret_cast<uint4*>(as)[q] = src[q];
     __syncthreads();
-  });
+  };
+  const int fmt = slot_format(p.scale_fmt, ent, is_shared);
+  if (is_shared) {  // the shared expert's two step ranges, added
+    const int half = shared_down_half(p.i);
+    f32x4 acc1 = {0, 0, 0, 0};
+    down_slot(fmt, ent, as, p.m, p.i, p.d, r0, 0, half, acc, stage);
+    down_slot(fmt, ent, as, p.m, p.i, p.d, r0, half, p.i / 128, acc1, []() {});
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = __fadd_rn(acc[c], acc1[c]);
+  } else {
+    down_slot(fmt, ent, as, p.m, p.i, p.d, r0, acc, stage);
+  }
   // lane (col = lane%16) holds rows 4*(lane/16)+q; column t (hi) + column m+t (lo)
   // of token t are combined through the lane that owns column t.
   // Cross-block handoff without cache flushes: partials are written with

@@ -15,8 +15,9 @@
 //        launch's tag, in kScoreCopies copies
 //   SGU  shared-expert gate or up: 16 rows of W1 or of W3 per item, the rows'
 //        fp32 sums published for the shared down
-//   SD   shared-expert down, 64 rows of W2 per item (ahead of the routed
-//        items: its weights stream while the routing is still being decided)
+//   SD   shared-expert down, 32 rows of W2 per item, each over both halves of
+//        the steps (two waves per half: an FP8 row is twice an FP4 one, so
+//        an item streams what a routed down item does)
 //   GU   routed gate/up, (slot, 16 rows) per item; needs the slot plan
 //   D    routed down, (slot, 64 rows) per item
 // Every workgroup that runs a routed item (or the shared down) builds the slot
@@ -68,8 +69,9 @@ constexpr int kCtlDone = 128;    // workgroups finished
 constexpr int kCtlErr = 192;     // sticky: 1 + the code of a wait that gave up:
 constexpr int kWaitScores = 4608;  //   a plan's wait for the router scores
 constexpr int kWaitAct = 4609;     //   a down item's wait for its slot's activations
-constexpr int kWaitShared = 4610;  //   the shared down's wait for the gate and up sums
+constexpr int kWaitShared = 4610;  //   the shared down's wait for the shared activations
 constexpr int kWaitPart = 4611;    //   a row group's wait for the slots' partials
+constexpr int kWaitGate = 4612;    //   a shared up item's wait for its rows' gate sums
 constexpr int kMaxRowGroups = 2048;
 constexpr size_t kCtlBytes = 4096;
 // Once a launch's tag reaches kRearmTag its last workgroup zeroes the tagged
@@ -99,7 +101,7 @@ struct LayerParams {
   uint64_t* scores;     // kScoreCopies copies of [m][n_exp] tagged fp32 scores
   int score_stride;     // 64-bit words between copies
   uint64_t* act;   // tagged [S][m][i] weighted activations of the routed slots
-  uint64_t* sgh;   // tagged [2][m][i] shared expert gate (0) and up (1) row sums
+  uint64_t* sgh;   // tagged [2][m][i] shared expert gate row sums (0) and activations (1)
   uint64_t* part;  // tagged [S + 1][m][d] per-slot down partials (slot S: shared)
   uint4* wipe;      // the workspace after the control words, zeroed at a re-arm
   int64_t wipe_n;   //   (16-byte units)
@@ -115,6 +117,10 @@ struct LayerParams {
   // item ranges [start, end): R is [0, n_router); the others follow in an
   // order where every item's producers come before it
   int n_router, sgu0, sgu1, sd0, sd1, gu0, gu1, d0, d1, n_items;
+  // routed down items in pairs (drun = 2; else 1): in each block of 2 * dgrid
+  // items, dk slots whose row groups a workgroup takes two at a time, so
+  // that its second item reuses the staged activations of its first
+  int drun, dgrid, dk;
 };
 
 // This launch's tag: the previous launch's plus one (never 0).  The epoch word
@@ -174,6 +180,7 @@ struct Shared {
   alignas(4) unsigned char used[kMaxExperts];   // expert e is selected by some token (plan build)
   short rank[kMaxExperts];                      // slot of a selected expert (plan build)
 };
+static_assert(sizeof(Shared::red) >= 2 * 64 * 4 * sizeof(float), "shared down: two waves' accumulators");
 
 // The router part of the slot plan: wave w takes the top-k of tokens w,
 // w + kWaves (ties to the lower index) from the tokens' tagged scores, polled
@@ -500,18 +507,25 @@ __device__ __noinline__ int gate_up_item(uint64_t kernarg, int q_arg, int state_
   return state;
 }
 
-// Shared gate/up, one matrix per item: item k streams rows 16*(k/2) .. +15 of
-// W1 (k even) or W3 (k odd) -- one matrix, so twice the steps per batch of a
-// routed gate/up item in the same registers -- and publishes the rows' fp32
-// sums (the four waves' K ranges added in wave order, as gate_up_item adds
-// them) to p.sgh; the shared down applies the SwiGLU when it stages them.
+// Shared gate/up, one matrix per item: item k streams the 16 rows of one row
+// group of W1 or W3 -- one matrix, so twice the steps per batch of a routed
+// gate/up item in the same registers -- and adds the four waves' K ranges in
+// wave order, as gate_up_item does.  Items come in blocks of 8 row groups: W1
+// of the 8 groups, then W3 of the same 8 (a short last block likewise).  The
+// W1 item publishes its rows' gate sums to plane 0 of p.sgh; the W3 item (a
+// larger item index, running beside it) waits for them and publishes the
+// rows' activations SwiGLU(gate, up) (weight 1) to plane 1, which the shared
+// down stages as a routed down stages its slot's.
 __device__ __noinline__ int shared_half_item(uint64_t kernarg, int q_arg, int state_arg) {
   const int q = __builtin_amdgcn_readfirstlane(q_arg);
   int state = __builtin_amdgcn_readfirstlane(state_arg);
   const LayerParams p = params(kernarg);
   Shared& sh = g_sh;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int k = q - p.sgu0, mat = k & 1, r0 = (k >> 1) * kGuRows;
+  // the W1 and W3 items of a row group are `span` (8) item indices apart, so
+  // that they run on one XCD when workgroups are dealt to the 8 XCDs in turn
+  const int k = q - p.sgu0, blk = k >> 4, span = min(8, p.i / kGuRows - 8 * blk);
+  const int mat = (k & 15) >= span, r0 = (8 * blk + (k & 15) - mat * span) * kGuRows;
   const unsigned tag = launch_tag(p.ctl);
   const uint64_t* ent = sh.ent[p.S];
   ensure_x(p, state);
@@ -533,7 +547,15 @@ __device__ __noinline__ int shared_half_item(uint64_t kernarg, int q_arg, int st
     float sum = 0.0f;
 #pragma unroll
     for (int w4 = 0; w4 < kWaves; ++w4) sum = __fadd_rn(sum, sh.red[w4][0][row * kMaxTok + col]);
-    store_agent(p.sgh + ((int64_t)mat * p.m + col) * p.i + r0 + row, tagged(tag, __float_as_uint(sum)));
+    const uint32_t off = (uint32_t)(col * p.i + r0 + row);
+    if (mat == 0) {
+      store_agent(p.sgh + off, tagged(tag, __float_as_uint(sum)));
+    } else {
+      float gv[1];
+      poll_tagged<1>(p.sgh, 0, off, 1, tag, gv, p.ctl, kWaitGate);
+      const float a = __fmul_rn(1.0f, swiglu(gv[0], sum, p.limit));
+      store_agent(p.sgh + (int64_t)p.m * p.i + off, tagged(tag, __float_as_uint(a)));
+    }
   }
   return state;
 }
@@ -622,13 +644,52 @@ __device__ __noinline__ int gate_up_run(uint64_t kernarg, int q_arg, int state_a
   return q;
 }
 
-// Slot and row group of down item q (shared down items first).
-__device__ __forceinline__ void down_slot_of(const LayerParams& p, int q, bool& is_shared, int& s, int& g) {
-  const int down_per_slot = p.d / kDownRows;
+// Slot, row group (kDownRows rows) and half of down item q: a routed down
+// item covers its row group (h = 0); shared down items 2g + h cover rows
+// 32h .. 32h + 31 of row group g, two waves per step range of the shared
+// expert's split (shared_down_half).  Routed down items: with drun = 2,
+// blocks of 2G items (G = dgrid) for dk slots each -- in a block, column c
+// (item c and item c + G, which workgroup (d0 + c) % G runs one after the
+// other) takes row groups c % half and half + c % half (half = groups per
+// slot / 2) of slot c / half -- then the slots left, slot-major.
+__device__ __forceinline__ void down_slot_of(const LayerParams& p, int q, bool& is_shared, int& s, int& g, int& h) {
+  const int dps = p.d / kDownRows;
   is_shared = q >= p.sd0 && q < p.sd1;
-  const int qq = is_shared ? q - p.sd0 : q - p.d0;
-  s = is_shared ? p.S : qq / down_per_slot;
-  g = qq % down_per_slot;
+  h = 0;
+  if (is_shared) {
+    s = p.S;
+    g = (q - p.sd0) >> 1;
+    h = (q - p.sd0) & 1;
+    return;
+  }
+  int u = q - p.d0, s0 = 0;
+  if (p.drun == 2) {
+    const int G = p.dgrid, half = dps / 2, nb = p.S / p.dk;
+    if (u < nb * 2 * G) {
+      const int b = u / (2 * G), pp = u - b * 2 * G, r = pp >= G ? 1 : 0, c = pp - r * G;
+      s = b * p.dk + c / half;
+      g = r * half + c % half;
+      return;
+    }
+    u -= nb * 2 * G;
+    s0 = nb * p.dk;
+  }
+  s = s0 + u / dps;
+  g = u % dps;
+}
+
+// Item index of routed down item (slot s, row group g): increasing in s.
+__device__ __forceinline__ int down_index(const LayerParams& p, int s, int g) {
+  const int dps = p.d / kDownRows;
+  if (p.drun == 2) {
+    const int G = p.dgrid, half = dps / 2, nb = p.S / p.dk;
+    if (s < nb * p.dk) {
+      const int b = s / p.dk;
+      return p.d0 + b * 2 * G + (g / half) * G + (s - b * p.dk) * half + g % half;
+    }
+    return p.d0 + nb * 2 * G + (s - nb * p.dk) * dps + g;
+  }
+  return p.d0 + s * dps + g;
 }
 
 // Down item q, first part: W2 rows of the slot against its activations, the
@@ -644,28 +705,28 @@ __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg
   Shared& sh = g_sh;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   bool is_shared_q;
-  int s, g;
-  down_slot_of(p, q, is_shared_q, s, g);
+  int s, g, h;
+  down_slot_of(p, q, is_shared_q, s, g, h);
   constexpr bool is_shared = kShared;
   if (!is_shared && s >= sh.n_routed) return state;
   const unsigned tag = launch_tag(p.ctl);  // (issued before the weight loads)
   const uint64_t* ent = sh.ent[s];
-  const int r0 = g * kDownRows + 16 * wave;
+  // shared: waves 0 and 2 (1 and 3) take rows r0 .. r0 + 15 over the first
+  // (second) step range
+  const int r0 = kShared ? g * kDownRows + 32 * h + 16 * (wave & 1) : g * kDownRows + 16 * wave;
   const int m = p.m, i = p.i;
   unsigned* const ctl = p.ctl;
   const uint64_t* const src = p.act + (int64_t)s * m * i;
   const uint64_t* const sgh = p.sgh;
-  const float limit = p.limit;
   f32x4 acc = {0, 0, 0, 0};
   auto stage = [&]() __attribute__((always_inline)) {
-    // fp32 activations -> bf16 hi rows [t][k] and lo rows [m + t][k], each
-    // written once it carries this launch's tag;
-    // the shared slot's are the SwiGLU of its published gate and up sums
-    // (weight 1)
+    // fp32 activations (the shared slot's: plane 1 of p.sgh) -> bf16 hi
+    // rows [t][k] and lo rows [m + t][k], each written once it carries this
+    // launch's tag -- unless the tile holds them from this workgroup's
+    // previous item
+    if (!kShared && state == 2 + s) return;
     const int n = m * i;
-    // per thread and round (registers: the W2 batch is live; the shared slot
-    // reads two planes per word)
-    constexpr int kStageWords = kShared ? 4 : 8;
+    constexpr int kStageWords = 8;  // per thread and round (registers: the W2 batch is live)
     for (int u0 = 0; u0 < n; u0 += kStageWords * kThreads) {  // this thread's words u0 + threadIdx.x + kThreads * j
       const int c0 = u0 + (int)threadIdx.x;
       unsigned need = 0;
@@ -674,19 +735,17 @@ __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg
         if (c0 + kThreads * j < n) need |= 1u << j;
       for (unsigned it = 0; it < kSpinLimit; ++it) {
         const unsigned cur = need;  // every load of the round in flight at once
-        uint64_t w[kStageWords], wu[kStageWords];
+        uint64_t w[kStageWords];
 #pragma unroll
         for (int j = 0; j < kStageWords; ++j) {
-          const uint64_t* b = is_shared ? sgh : src;
+          const uint64_t* b = is_shared ? sgh + n : src;
           w[j] = (cur >> j) & 1u ? load_agent(b + u0 + kThreads * j + threadIdx.x) : 0ull;
-          wu[j] = is_shared && ((cur >> j) & 1u) ? load_agent(sgh + n + u0 + kThreads * j + threadIdx.x) : 0ull;
         }
 #pragma unroll
         for (int j = 0; j < kStageWords; ++j) {
-          const bool fresh = (unsigned)(w[j] >> 32) == tag && (!is_shared || (unsigned)(wu[j] >> 32) == tag);
+          const bool fresh = (unsigned)(w[j] >> 32) == tag;
           if (((cur >> j) & 1u) && fresh) {
-            const float v = __uint_as_float((unsigned)w[j]);
-            const float a = is_shared ? __fmul_rn(1.0f, swiglu(v, __uint_as_float((unsigned)wu[j]), limit)) : v;
+            const float a = __uint_as_float((unsigned)w[j]);
             const int c = c0 + kThreads * j;
             const uint32_t hi = f32_to_bf16_bits(a);
             const uint32_t lo = f32_to_bf16_bits(__fadd_rn(a, -bf16_bits_to_f32(hi)));
@@ -712,17 +771,30 @@ __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg
   };
   const int fmt = slot_format(p.scale_fmt, ent, is_shared);
   if constexpr (kShared) {
-    if (fmt == kFp8Block) down_any<kFp8Block, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
-    else down_any<kBf16, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
+    const int half = shared_down_half(i), st0 = wave < 2 ? 0 : half, st1 = wave < 2 ? half : i / 128;
+    if (fmt == kFp8Block) down_any<kFp8Block, true>(ent, g_tile, m, i, p.d, r0, st0, st1, acc, stage);
+    else down_any<kBf16, true>(ent, g_tile, m, i, p.d, r0, st0, st1, acc, stage);
+    // first range + second range, in the waves of the first
+    float* const xr = &sh.red[0][0][0];
+    if (wave >= 2) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xr[((wave - 2) * 64 + lane) * 4 + c] = acc[c];
+    }
+    __syncthreads();
+    if (wave < 2) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] = __fadd_rn(acc[c], xr[(wave * 64 + lane) * 4 + c]);
+    }
   } else {
     if (fmt == kFp4E8M0) down_any<kFp4E8M0, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
     else if (fmt == kFp4F32) down_any<kFp4F32, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
     else down_any<kBf16, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
   }
-  state = 0;
+  state = kShared ? 0 : 2 + s;
   // lane (col = lane%16) holds rows 4*(lane/16)+c; column t (hi) + column m+t (lo)
   // of token t are combined through the lane that owns column t.
   uint64_t* part = p.part + (int64_t)s * m * p.d;
+  if (kShared && wave >= 2) return state;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int col = lane & 15;
@@ -743,13 +815,12 @@ __device__ __noinline__ void down_finish(uint64_t kernarg, int q_arg) {
   const LayerParams p = params(kernarg);
   Shared& sh = g_sh;
   bool is_shared;
-  int s, g;
-  down_slot_of(p, q, is_shared, s, g);
+  int s, g, h;
+  down_slot_of(p, q, is_shared, s, g, h);
   const int n_routed = sh.n_routed;
   if (!is_shared && s >= n_routed) return;
-  const int dps = p.d / kDownRows;
-  int last = n_routed > 0 ? p.d0 + (n_routed - 1) * dps + g : -1;
-  if (p.shared && p.sd0 + g > last) last = p.sd0 + g;
+  int last = n_routed > 0 ? down_index(p, n_routed - 1, g) : -1;
+  if (p.shared && p.sd0 + 2 * g + 1 > last) last = p.sd0 + 2 * g + 1;
   if (q != last) return;
   const unsigned tag = launch_tag(p.ctl);
   const int m = p.m;
@@ -781,7 +852,7 @@ __device__ __noinline__ void down_finish(uint64_t kernarg, int q_arg) {
 }
 
 __global__ void __launch_bounds__(kThreads, 2) moe_layer_kernel(LayerParams p) {
-  int state = 0;  // 1 while the LDS tile holds x
+  int state = 0;  // 1 while the LDS tile holds x, 2 + s while routed slot s's activations
   if (threadIdx.x == 0) g_sh.have_plan = 0;
   if (p.shared && threadIdx.x < 6) g_sh.ent[p.S][threadIdx.x] = ldg<uint64_t>(p.shared + threadIdx.x);
   const uint64_t kernarg = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();  // &p
@@ -990,7 +1061,7 @@ int launch_layer(const char* name, const void* x, int64_t m, int64_t d, int64_t 
   // early enough that the shared down, which nothing waits for but the
   // output sums, is better spent filling the last round (measured: M=1
   // 42 us instead of 47; M=3 88 us instead of 93).
-  const int n_sgu = has_shared * 2 * (int)(i / kGuRows), n_sd = has_shared * (int)(d / kDownRows);
+  const int n_sgu = has_shared * 2 * (int)(i / kGuRows), n_sd = has_shared * 2 * (int)(d / kDownRows);
   const int n_gu = p.S * (int)(i / kGuRows), n_d = p.S * (int)(d / kDownRows);
   p.sgu0 = p.n_router;
   p.sgu1 = p.sgu0 + n_sgu;
@@ -1014,6 +1085,16 @@ int launch_layer(const char* name, const void* x, int64_t m, int64_t d, int64_t 
   int rc = resident_workgroups(lds, &resident);
   if (rc) return rc;
   const int grid = resident < p.n_items ? resident : p.n_items;
+  // routed down items in pairs when two full rounds of them exist and the
+  // grid splits into whole slots of half-slot columns
+  const int dps = (int)(d / kDownRows);
+  p.drun = 1;
+  p.dgrid = grid;
+  p.dk = 0;
+  if (n_d >= 2 * grid && dps % 2 == 0 && grid % (dps / 2) == 0) {
+    p.drun = 2;
+    p.dk = 2 * grid / dps;
+  }
   hipLaunchKernelGGL(moe_layer_kernel, dim3((unsigned)grid), dim3(kThreads), lds, stream, p);
   return check_launch(name);
 }

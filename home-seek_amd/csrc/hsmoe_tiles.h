@@ -278,29 +278,29 @@ __device__ __forceinline__ float swiglu(float gsum, float usum, float L) {
 }
 
 // ------------------------------------------------------------ down
-// One wave: rows r0..r0+15 of W2 ([d][i]) of the slot `ent` over all i/128
-// steps against the activation tile as ([2m][i] bf16 in LDS: hi rows then lo
-// rows).  `ready()` runs (block-wide) after the first batch's loads are issued
-// and before the tile is read, so the weight loads overlap whatever it waits
-// for.
+// One wave: rows r0..r0+15 of W2 ([d][i]) of the slot `ent` over steps
+// [st0, st1) of the i/128 against the activation tile as ([2m][i] bf16 in
+// LDS: hi rows then lo rows).  `ready()` runs (block-wide) after the first
+// batch's loads are issued and before the tile is read, so the weight loads
+// overlap whatever it waits for.
 template <int F, int kB, typename Ready>
 __device__ __forceinline__ void down_rows(const uint64_t* ent, const uint16_t* as, int m, int i, int d, int r0,
-                                          f32x4& acc, Ready&& ready) {
+                                          int st0, int st1, f32x4& acc, Ready&& ready) {
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int row = r0 + r;
-  const int n = i / 128;
   const Mat w2 = make_mat<F>(ent[4], ent[5], d, i);
   Batch<F, kB> bw;
-  bw.load(w2, row, i, 0, g);
+  if (st0 < st1) bw.load(w2, row, i, st0, g);
   ready();
+  if (st0 >= st1) return;  // (an empty range: the sum stays zero)
   Frags ac;
-  ac.read(as, i, r, g, 0, 2 * m);
-  for (int st = 0; st < n; st += kB) {
-    if (st) bw.load(w2, row, i, st, g);
+  ac.read(as, i, r, g, st0, 2 * m);
+  for (int st = st0; st < st1; st += kB) {
+    if (st != st0) bw.load(w2, row, i, st, g);
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
       Frags an;
-      an.read(as, i, r, g, min(st + b + 1, n - 1), 2 * m);
+      an.read(as, i, r, g, min(st + b + 1, st1 - 1), 2 * m);
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc = mfma16x16x32(bw.frag(b, j, g), ac.f[j], acc);
       ac = an;
@@ -310,15 +310,26 @@ __device__ __forceinline__ void down_rows(const uint64_t* ent, const uint16_t* a
 
 template <int F, bool kDeep, typename Ready>
 __device__ __forceinline__ void down_any(const uint64_t* ent, const uint16_t* as, int m, int i, int d, int r0,
-                                         f32x4& acc, Ready&& ready) {
+                                         int st0, int st1, f32x4& acc, Ready&& ready) {
   constexpr int kMax = down_batch<F, kDeep>();
-  const int b = batch_for<kMax>(i / 128);
-  if (b == kMax) down_rows<F, kMax>(ent, as, m, i, d, r0, acc, ready);
-  else if (kMax > 8 && b == 8) down_rows<F, (kMax > 8 ? 8 : 1)>(ent, as, m, i, d, r0, acc, ready);
-  else if (kMax > 4 && b == 4) down_rows<F, (kMax > 4 ? 4 : 1)>(ent, as, m, i, d, r0, acc, ready);
-  else if (kMax > 2 && b == 2) down_rows<F, (kMax > 2 ? 2 : 1)>(ent, as, m, i, d, r0, acc, ready);
-  else down_rows<F, 1>(ent, as, m, i, d, r0, acc, ready);
+  const int b = batch_for<kMax>(st1 - st0);
+  if (b == kMax) down_rows<F, kMax>(ent, as, m, i, d, r0, st0, st1, acc, ready);
+  else if (kMax > 8 && b == 8) down_rows<F, (kMax > 8 ? 8 : 1)>(ent, as, m, i, d, r0, st0, st1, acc, ready);
+  else if (kMax > 4 && b == 4) down_rows<F, (kMax > 4 ? 4 : 1)>(ent, as, m, i, d, r0, st0, st1, acc, ready);
+  else if (kMax > 2 && b == 2) down_rows<F, (kMax > 2 ? 2 : 1)>(ent, as, m, i, d, r0, st0, st1, acc, ready);
+  else down_rows<F, 1>(ent, as, m, i, d, r0, st0, st1, acc, ready);
 }
+
+template <int F, bool kDeep, typename Ready>
+__device__ __forceinline__ void down_any(const uint64_t* ent, const uint16_t* as, int m, int i, int d, int r0,
+                                         f32x4& acc, Ready&& ready) {
+  down_any<F, kDeep>(ent, as, m, i, d, r0, 0, i / 128, acc, ready);
+}
+
+// The shared expert's split of the i/128 down steps: [0, half) and
+// [half, i/128), each accumulated from zero, the two sums added (first +
+// second) -- one split for every path, so that they agree bit for bit.
+__device__ __forceinline__ int shared_down_half(int i) { return (i / 128) / 2; }
 
 template <bool kDeep = false, typename Ready>
 __device__ __forceinline__ void down_slot(int fmt, const uint64_t* ent, const uint16_t* as, int m, int i, int d,
@@ -328,6 +339,18 @@ __device__ __forceinline__ void down_slot(int fmt, const uint64_t* ent, const ui
     case kFp4F32: down_any<kFp4F32, kDeep>(ent, as, m, i, d, r0, acc, ready); break;
     case kFp8Block: down_any<kFp8Block, kDeep>(ent, as, m, i, d, r0, acc, ready); break;
     default: down_any<kBf16, kDeep>(ent, as, m, i, d, r0, acc, ready); break;
+  }
+}
+
+// down_slot over steps [st0, st1) only.
+template <bool kDeep = false, typename Ready>
+__device__ __forceinline__ void down_slot(int fmt, const uint64_t* ent, const uint16_t* as, int m, int i, int d,
+                                          int r0, int st0, int st1, f32x4& acc, Ready&& ready) {
+  switch (fmt) {
+    case kFp4E8M0: down_any<kFp4E8M0, kDeep>(ent, as, m, i, d, r0, st0, st1, acc, ready); break;
+    case kFp4F32: down_any<kFp4F32, kDeep>(ent, as, m, i, d, r0, st0, st1, acc, ready); break;
+    case kFp8Block: down_any<kFp8Block, kDeep>(ent, as, m, i, d, r0, st0, st1, acc, ready); break;
+    default: down_any<kBf16, kDeep>(ent, as, m, i, d, r0, st0, st1, acc, ready); break;
   }
 }
 
