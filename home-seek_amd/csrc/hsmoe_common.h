@@ -61,6 +61,10 @@ __device__ __forceinline__ uint32_t bload32(BufRsrc r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
 __device__ __forceinline__ float bloadf(BufRsrc r, uint32_t off) { return __uint_as_float(bload32(r, off)); }
+__device__ __forceinline__ uint2 bload64(BufRsrc r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+  return make_uint2(v[0], v[1]);
+}
 __device__ __forceinline__ uint32_t bload8(BufRsrc r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
 }

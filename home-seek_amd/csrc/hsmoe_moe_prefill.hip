@@ -357,7 +357,8 @@ __device__ void gate_up_chunk(const PrefillParams& p, const Chunk& ch, int r0, u
 // F: format of the chunks' weights (routed FP4 of the call's scale kind, or
 // the shared expert's FP8); table entries without scales take the bf16 path.
 template <int F, bool kShared>
-__global__ void __launch_bounds__(kThreads) prefill_gate_up_kernel(PrefillParams p) {
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(F == kFp8Block ? 2 : 4)))
+prefill_gate_up_kernel(PrefillParams p) {
   __shared__ __align__(16) uint16_t xs[kChunk * (kCols + kPad)];
   __shared__ int s_tok[kChunk];
   const int nrb = p.i / kGuRows;

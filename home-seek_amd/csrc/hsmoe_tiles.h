@@ -52,7 +52,7 @@ template <int kB>
 struct Batch<kFp4E8M0, kB> {
   uint4 a[kB];
   uint4 sq[kB >= 4 ? kB / 4 : 1];  // kB >= 4: 16 scale bytes per 4 steps (bytes 4b..4b+3 = step b)
-  uint32_t sb[kB];                 // kB < 4: one scale byte per step
+  uint32_t sw[kB];                 // kB < 4: the 4 scale bytes of each step (byte g = group g)
   __device__ __forceinline__ void load(const Mat& m, int row, int k, int st, int g) {
     const uint32_t wo = (uint32_t)row * (uint32_t)(k / 2) + st * 64 + g * 16;
 #pragma unroll
@@ -61,9 +61,12 @@ struct Batch<kFp4E8M0, kB> {
     if constexpr (kB >= 4) {
 #pragma unroll
       for (int q = 0; q < kB / 4; ++q) sq[q] = bload128(m.s, so + 16 * q);
+    } else if constexpr (kB == 2) {  // both steps' scale words in one load
+      const uint2 w2 = bload64(m.s, so);
+      sw[0] = w2.x;
+      sw[1] = w2.y;
     } else {
-#pragma unroll
-      for (int b = 0; b < kB; ++b) sb[b] = bload8(m.s, so + 4 * b + g);
+      sw[0] = bload32(m.s, so);
     }
   }
   __device__ __forceinline__ bf16x8 frag(int b, int j, int g) const {
@@ -76,7 +79,7 @@ struct Batch<kFp4E8M0, kB> {
       const uint32_t word = d == 0 ? s4.x : d == 1 ? s4.y : d == 2 ? s4.z : s4.w;
       e = (word >> (8 * g)) & 0xffu;
     } else {
-      e = sb[b];
+      e = (sw[b] >> (8 * g)) & 0xffu;
     }
     return fp4x8_to_bf16_e8m0(dw, e8m0_as_f32(e));
   }
