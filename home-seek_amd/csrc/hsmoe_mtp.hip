@@ -24,6 +24,7 @@ constexpr int kMaxTok = 8;
 constexpr int kWaves = 8;
 constexpr int kRowsPerBlock = 64 * kWaves;
 constexpr size_t kLdsHBytes = 128 * 1024;  // hidden states in LDS up to this size (one workgroup per CU)
+constexpr int kMfmaMinTok = 2;  // the fp64 MFMA form serves 2..4 tokens (one token: the row-per-lane form)
 
 struct Workspace {
   unsigned long long key[kMaxTok];
@@ -44,6 +45,144 @@ __device__ __forceinline__ unsigned long long logit_key(uint32_t bits, int64_t v
   uint32_t o = (bits & 0x8000u) ? (~bits & 0xffffu) : (bits | 0x8000u);
   if ((bits & 0x7fffu) > 0x7f80u) o = 0x1ffffu;  // NaN: torch.argmax returns the first NaN
   return ((unsigned long long)o << 32) | (unsigned long long)(0xffffffffu - (uint32_t)v);
+}
+
+// The acceptance rule, in the last workgroup to arrive (thread 0): pred[t]
+// from the vocab-wide keys (cleared for the next call), the longest prefix of
+// ids[1..] equal to pred[0..], the counter re-armed.
+template <int kTok>
+__device__ void accept_tail(const int64_t* __restrict__ ids, int64_t* __restrict__ pred_out,
+                            int64_t* __restrict__ result_out, Workspace* __restrict__ ws) {
+  int64_t pred[kTok];
+#pragma unroll
+  for (int t = 0; t < kTok; ++t) {
+    const unsigned long long k = __hip_atomic_exchange(&ws->key[t], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    pred[t] = (int64_t)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
+    pred_out[t] = pred[t];
+  }
+  int64_t n_acc = 0;
+  for (int t = 0; t + 1 < kTok; ++t) {
+    if (pred[t] != ids[t + 1]) break;
+    ++n_acc;
+  }
+  result_out[0] = n_acc;
+  result_out[1] = n_acc;
+  __hip_atomic_store(&ws->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------- fp64 MFMA form
+// For up to 4 tokens the dot products run on v_mfma_f64_4x4x4_4b_f64: four
+// blocks of D (4x4) += A (4x4) B (4x4) in fp64 per instruction, operands
+// (fitted on the device) A_b[i][k] in lane 16k + 4b + i, B_b[k][j] in lane
+// 16k + 4b + j, D_b[i][j] in lane 16i + 4b + j.  A wave owns 16 vocab rows
+// (block b, row i = vocab row 4b + i of the wave's 16) and the 4 token
+// columns j (tokens past n_tok are zero); with W = kMfmaW, its k-slot k at
+// instruction n of group g is column 32W g + 8W k + n, so that each lane
+// reads 8W consecutive weights (W 16-byte loads) per group, and a row's 64W
+// bytes of a group come from its 4 lanes (HBM streams contiguous rows
+// better: 64 bytes per row and group ran at 4.15 TB/s, 128 bytes at 4.5).
+// The hidden states sit in LDS as bf16 [4][d]; a B lane reads its 8W values
+// of a group in W 16-byte LDS loads.  Products of
+// bf16 values are exact in fp64 and every partial sum is a subset sum of a
+// row's products, so a logit is the row's exact sum rounded once to bf16
+// whenever that sum is exact in fp64, as for the row-per-lane form.
+constexpr int kMfmaWaves = 4;
+constexpr int kMfmaW = 2;                  // 16-byte loads per lane and group (8 k each)
+constexpr int kMfmaAhead = 16 / kMfmaW;    // groups in flight per wave (256 bytes per lane)
+
+__device__ __forceinline__ double bf16_lane(const uint4& q, int n) {
+  const uint32_t word = n < 2 ? q.x : n < 4 ? q.y : n < 6 ? q.z : q.w;
+  return (double)__uint_as_float((n & 1) ? (word & 0xffff0000u) : (word << 16));
+}
+
+template <int kTok>
+__global__ void __launch_bounds__(64 * kMfmaWaves)
+    lm_head_mfma_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ h, int64_t d, int64_t vocab,
+                        const int64_t* __restrict__ ids, uint16_t* __restrict__ logits,
+                        int64_t* __restrict__ pred_out, int64_t* __restrict__ result_out,
+                        Workspace* __restrict__ ws) {
+  extern __shared__ uint16_t s_hb[];  // [4][d] bf16, rows >= kTok zero
+  __shared__ unsigned long long s_key[kMfmaWaves][4];
+  __shared__ int s_last;
+  const int chunks = (int)(d / 8);
+  for (int c = threadIdx.x; c < 4 * chunks; c += 64 * kMfmaWaves) {
+    const int t = c / chunks;
+    reinterpret_cast<uint4*>(s_hb)[c] = t < kTok ? reinterpret_cast<const uint4*>(h)[c] : make_uint4(0, 0, 0, 0);
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kk = lane >> 4, b = (lane >> 2) & 3, lo = lane & 3;
+  const int64_t base = ((int64_t)blockIdx.x * kMfmaWaves + wave) * 16;
+  const int64_t arow = base + 4 * b + lo < vocab ? base + 4 * b + lo : vocab - 1;  // (rows past the end: unused)
+  constexpr int kGk = 32 * kMfmaW;  // columns per group
+  const uint4* wq = reinterpret_cast<const uint4*>(w + arow * d + 8 * kMfmaW * kk);  // + 4 kMfmaW g: group g
+  const uint4* hq = reinterpret_cast<const uint4*>(s_hb + (int64_t)lo * d + 8 * kMfmaW * kk);
+  const int ng = (int)(d / kGk);
+  double acc0 = 0.0, acc1 = 0.0;
+  uint4 q[kMfmaAhead][kMfmaW];
+#pragma unroll
+  for (int p = 0; p < kMfmaAhead; ++p)
+#pragma unroll
+    for (int h2 = 0; h2 < kMfmaW; ++h2) q[p][h2] = p < ng ? wq[4 * kMfmaW * p + h2] : make_uint4(0, 0, 0, 0);
+  for (int g0 = 0; g0 < ng; g0 += kMfmaAhead) {
+#pragma unroll
+    for (int p = 0; p < kMfmaAhead; ++p) {
+      const int g = g0 + p;
+      if (g < ng) {
+#pragma unroll
+        for (int h2 = 0; h2 < kMfmaW; ++h2) {
+          const uint4 cur = q[p][h2];
+          if (g + kMfmaAhead < ng) q[p][h2] = wq[4 * kMfmaW * (g + kMfmaAhead) + h2];
+          const uint4 hv = hq[4 * kMfmaW * g + h2];
+#pragma unroll
+          for (int n = 0; n < 8; n += 2) {
+            acc0 = __builtin_amdgcn_mfma_f64_4x4x4f64(bf16_lane(cur, n), bf16_lane(hv, n), acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f64_4x4x4f64(bf16_lane(cur, n + 1), bf16_lane(hv, n + 1), acc1, 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+  // lane (i = kk, b, j = lo): row base + 4b + i, token j
+  const int64_t v = base + 4 * b + kk;
+  const int t = lo;
+  unsigned long long key = 0;
+  if (t < kTok && v < vocab) {
+    const uint32_t bits = f64_to_bf16_bits(acc0 + acc1);
+    if (logits) logits[t * vocab + v] = (uint16_t)bits;
+    key = logit_key(bits, v);
+  }
+  // the wave's best key of token lo: lanes with equal lane & 3
+#pragma unroll
+  for (int off = 4; off < 64; off <<= 1) {
+    const unsigned long long o = __shfl_xor(key, off, 64);
+    key = o > key ? o : key;
+  }
+  if (lane < 4) s_key[wave][lane] = key;
+  __syncthreads();
+  if (threadIdx.x < kTok) {
+    unsigned long long k = 0;
+#pragma unroll
+    for (int q2 = 0; q2 < kMfmaWaves; ++q2) k = s_key[q2][threadIdx.x] > k ? s_key[q2][threadIdx.x] : k;
+    __hip_atomic_fetch_max(&ws->key[threadIdx.x], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(&ws->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+  __syncthreads();
+  if (s_last && threadIdx.x == 0) accept_tail<kTok>(ids, pred_out, result_out, ws);
+}
+
+template <int kTok>
+int launch_mfma(const uint16_t* w, const uint16_t* h, int64_t d, int64_t vocab, const int64_t* ids, uint16_t* logits,
+                int64_t* pred, int64_t* result, Workspace* ws, hipStream_t st) {
+  const int64_t rows = 16 * kMfmaWaves;
+  const unsigned nb = (unsigned)((vocab + rows - 1) / rows);
+  const size_t lds = (size_t)4 * (size_t)d * 2;
+  hipLaunchKernelGGL((lm_head_mfma_kernel<kTok>), dim3(nb), dim3(64 * kMfmaWaves), lds, st, w, h, d, vocab, ids,
+                     logits, pred, result, ws);
+  return check_launch("hsmoe_lm_head_accept");
 }
 
 extern __shared__ double s_h[];  // [kTok][d] when kLds
@@ -135,21 +274,7 @@ __global__ void __launch_bounds__(64 * kWaves)
     s_last = __hip_atomic_fetch_add(&ws->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
   __syncthreads();
   if (!s_last || threadIdx.x != 0) return;
-  int64_t pred[kTok];
-#pragma unroll
-  for (int t = 0; t < kTok; ++t) {
-    const unsigned long long k = __hip_atomic_exchange(&ws->key[t], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    pred[t] = (int64_t)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
-    pred_out[t] = pred[t];
-  }
-  int64_t n_acc = 0;
-  for (int t = 0; t + 1 < kTok; ++t) {
-    if (pred[t] != ids[t + 1]) break;
-    ++n_acc;
-  }
-  result_out[0] = n_acc;
-  result_out[1] = n_acc;
-  __hip_atomic_store(&ws->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  accept_tail<kTok>(ids, pred_out, result_out, ws);
 }
 
 template <int kTok>
@@ -200,13 +325,22 @@ extern "C" int hsmoe_lm_head_accept(const void* h, const void* lm_head, int64_t 
                 hsmoe_lm_head_workspace_size(n_tok, vocab));
   hipStream_t st = (hipStream_t)stream;
   Workspace* ws = (Workspace*)workspace;
+  const uint16_t* w = (const uint16_t*)lm_head;
+  uint16_t* lg = (uint16_t*)logits_out;
+  if (n_tok >= kMfmaMinTok && n_tok <= 4 && aligned(h, 16)) {
+    const uint16_t* hb = (const uint16_t*)h;
+    switch (n_tok) {
+      case 1: return launch_mfma<1>(w, hb, d, vocab, ids, lg, pred_out, result_out, ws, st);
+      case 2: return launch_mfma<2>(w, hb, d, vocab, ids, lg, pred_out, result_out, ws, st);
+      case 3: return launch_mfma<3>(w, hb, d, vocab, ids, lg, pred_out, result_out, ws, st);
+      default: return launch_mfma<4>(w, hb, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    }
+  }
   double* h64 = (double*)((char*)workspace + h64_offset());
   hipLaunchKernelGGL(widen_h_kernel, dim3((unsigned)((n_tok * d + 255) / 256)), dim3(256), 0, st, (const uint16_t*)h,
                      n_tok * d, h64);
   int rc = check_launch("hsmoe_lm_head_accept(widen)");
   if (rc) return rc;
-  const uint16_t* w = (const uint16_t*)lm_head;
-  uint16_t* lg = (uint16_t*)logits_out;
   switch (n_tok) {
     case 1: return launch<1>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
     case 2: return launch<2>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
