@@ -74,21 +74,27 @@ __device__ void accept_tail(const int64_t* __restrict__ ids, int64_t* __restrict
 // For up to 4 tokens the dot products run on v_mfma_f64_4x4x4_4b_f64: four
 // blocks of D (4x4) += A (4x4) B (4x4) in fp64 per instruction, operands
 // (fitted on the device) A_b[i][k] in lane 16k + 4b + i, B_b[k][j] in lane
-// 16k + 4b + j, D_b[i][j] in lane 16i + 4b + j.  A wave owns 16 vocab rows
-// (block b, row i = vocab row 4b + i of the wave's 16) and the 4 token
-// columns j (tokens past n_tok are zero); with W = kMfmaW, its k-slot k at
-// instruction n of group g is column 32W g + 8W k + n, so that each lane
-// reads 8W consecutive weights (W 16-byte loads) per group, and a row's 64W
-// bytes of a group come from its 4 lanes (HBM streams contiguous rows
-// better: 64 bytes per row and group ran at 4.15 TB/s, 128 bytes at 4.5).
-// The hidden states sit in LDS as bf16 [4][d]; a B lane reads its 8W values
-// of a group in W 16-byte LDS loads.  Products of
-// bf16 values are exact in fp64 and every partial sum is a subset sum of a
-// row's products, so a logit is the row's exact sum rounded once to bf16
-// whenever that sum is exact in fp64, as for the row-per-lane form.
+// 16k + 4b + j, D_b[i][j] in lane 16i + 4b + j.  A wave works through tiles
+// of 4 vocab rows (A row i = tile row i, lane bits 0..1) against the 4 token
+// columns j (tokens past n_tok are zero); the 16 (block, k) pairs of a row
+// (lane bits 2..5, "slot") take 16 consecutive 16-byte pieces of it, so one
+// load instruction reads 256 contiguous bytes of each of the 4 rows and a
+// group of W = kMfmaW loads 256 W bytes per row.  Each block sums its own
+// quarter of the columns; at the end of a row the 4 blocks' partials are
+// added across lanes.  HBM streams long contiguous runs per row best: 64
+// bytes per row and group over 16 rows ran at 4.15 TB/s, 128 bytes at 4.5,
+// 1 KB over 4 rows at 4.8.  Tiles are dealt to waves in contiguous runs
+// (tiles_per_wave), with the load pipeline running on across a wave's tiles.
+// The hidden states sit in LDS as bf16 [4][d]; a B lane reads the same
+// columns as its A lane in 16-byte LDS loads.  Products of bf16 values are
+// exact in fp64 and every partial sum is a subset sum of a row's products,
+// so a logit is the row's exact sum rounded once to bf16 whenever that sum is
+// exact in fp64, as for the row-per-lane form.
 constexpr int kMfmaWaves = 4;
-constexpr int kMfmaW = 2;                  // 16-byte loads per lane and group (8 k each)
+constexpr int kMfmaW = 4;                  // 16-byte loads per lane and group (8 k each)
 constexpr int kMfmaAhead = 16 / kMfmaW;    // groups in flight per wave (256 bytes per lane)
+constexpr int kMfmaGroupCols = 128 * kMfmaW;  // columns of a row per group
+constexpr int kMfmaResidentWaves = 4096;   // 256 CUs x 4 SIMDs x 4 waves
 
 __device__ __forceinline__ double bf16_lane(const uint4& q, int n) {
   const uint32_t word = n < 2 ? q.x : n < 4 ? q.y : n < 6 ? q.z : q.w;
@@ -98,7 +104,7 @@ __device__ __forceinline__ double bf16_lane(const uint4& q, int n) {
 template <int kTok>
 __global__ void __launch_bounds__(64 * kMfmaWaves)
     lm_head_mfma_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ h, int64_t d, int64_t vocab,
-                        const int64_t* __restrict__ ids, uint16_t* __restrict__ logits,
+                        int tiles_per_wave, const int64_t* __restrict__ ids, uint16_t* __restrict__ logits,
                         int64_t* __restrict__ pred_out, int64_t* __restrict__ result_out,
                         Workspace* __restrict__ ws) {
   extern __shared__ uint16_t s_hb[];  // [4][d] bf16, rows >= kTok zero
@@ -111,48 +117,75 @@ __global__ void __launch_bounds__(64 * kMfmaWaves)
   }
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int kk = lane >> 4, b = (lane >> 2) & 3, lo = lane & 3;
-  const int64_t base = ((int64_t)blockIdx.x * kMfmaWaves + wave) * 16;
-  const int64_t arow = base + 4 * b + lo < vocab ? base + 4 * b + lo : vocab - 1;  // (rows past the end: unused)
-  constexpr int kGk = 32 * kMfmaW;  // columns per group
-  const uint4* wq = reinterpret_cast<const uint4*>(w + arow * d + 8 * kMfmaW * kk);  // + 4 kMfmaW g: group g
-  const uint4* hq = reinterpret_cast<const uint4*>(s_hb + (int64_t)lo * d + 8 * kMfmaW * kk);
-  const int ng = (int)(d / kGk);
-  double acc0 = 0.0, acc1 = 0.0;
+  const int lo = lane & 3, slot = lane >> 2;  // A row i / B token j; (block, k) pair
+  const int64_t ntile = (vocab + 3) / 4;
+  const int64_t t0 = ((int64_t)blockIdx.x * kMfmaWaves + wave) * tiles_per_wave;
+  const int64_t t1 = t0 + tiles_per_wave < ntile ? t0 + tiles_per_wave : ntile;
+  const int ng = (int)(d / kMfmaGroupCols);
+  const int64_t nf = t1 > t0 ? (t1 - t0) * ng : 0;  // (tile, group) steps of this wave
+  const uint4* hq = reinterpret_cast<const uint4*>(s_hb + (int64_t)lo * d + 8 * slot);
+  auto row_ptr = [&](int64_t t) {  // rows past the end read the last row; their sums are dropped
+    const int64_t r = 4 * t + lo < vocab ? 4 * t + lo : vocab - 1;
+    return reinterpret_cast<const uint4*>(w + r * d + 8 * slot);
+  };
+  unsigned long long key = 0;
   uint4 q[kMfmaAhead][kMfmaW];
+  int64_t lt = t0;  // tile and group of the next load
+  int lg = 0;
+  const uint4* lp = row_ptr(lt);
 #pragma unroll
-  for (int p = 0; p < kMfmaAhead; ++p)
+  for (int p = 0; p < kMfmaAhead; ++p) {
 #pragma unroll
-    for (int h2 = 0; h2 < kMfmaW; ++h2) q[p][h2] = p < ng ? wq[4 * kMfmaW * p + h2] : make_uint4(0, 0, 0, 0);
-  for (int g0 = 0; g0 < ng; g0 += kMfmaAhead) {
+    for (int h2 = 0; h2 < kMfmaW; ++h2) q[p][h2] = p < nf ? lp[16 * (kMfmaW * lg + h2)] : make_uint4(0, 0, 0, 0);
+    if (p < nf && ++lg == ng) {
+      lg = 0;
+      lp = row_ptr(++lt);
+    }
+  }
+  double acc0 = 0.0, acc1 = 0.0;
+  int cg = 0;  // group of the step being summed
+  int64_t ct = t0;
+  for (int64_t f0 = 0; f0 < nf; f0 += kMfmaAhead) {
 #pragma unroll
     for (int p = 0; p < kMfmaAhead; ++p) {
-      const int g = g0 + p;
-      if (g < ng) {
+      if (f0 + p < nf) {
+        const bool more = f0 + p + kMfmaAhead < nf;
 #pragma unroll
         for (int h2 = 0; h2 < kMfmaW; ++h2) {
           const uint4 cur = q[p][h2];
-          if (g + kMfmaAhead < ng) q[p][h2] = wq[4 * kMfmaW * (g + kMfmaAhead) + h2];
-          const uint4 hv = hq[4 * kMfmaW * g + h2];
+          if (more) q[p][h2] = lp[16 * (kMfmaW * lg + h2)];
+          const uint4 hv = hq[16 * (kMfmaW * cg + h2)];
 #pragma unroll
           for (int n = 0; n < 8; n += 2) {
             acc0 = __builtin_amdgcn_mfma_f64_4x4x4f64(bf16_lane(cur, n), bf16_lane(hv, n), acc0, 0, 0, 0);
             acc1 = __builtin_amdgcn_mfma_f64_4x4x4f64(bf16_lane(cur, n + 1), bf16_lane(hv, n + 1), acc1, 0, 0, 0);
           }
         }
+        if (more && ++lg == ng) {
+          lg = 0;
+          lp = row_ptr(++lt);
+        }
+        if (++cg == ng) {
+          // lane (i, b, j): block b's partial of row 4 ct + i, token j; add the 4 blocks
+          double s = acc0 + acc1;
+          s = s + __shfl_xor(s, 4, 64);
+          s = s + __shfl_xor(s, 8, 64);
+          const int64_t v = 4 * ct + (lane >> 4);
+          if ((lane & 12) == 0 && lo < kTok && v < vocab) {
+            const uint32_t bits = f64_to_bf16_bits(s);
+            if (logits) logits[lo * vocab + v] = (uint16_t)bits;
+            const unsigned long long k1 = logit_key(bits, v);
+            key = k1 > key ? k1 : key;
+          }
+          acc0 = 0.0;
+          acc1 = 0.0;
+          cg = 0;
+          ++ct;
+        }
       }
     }
   }
-  // lane (i = kk, b, j = lo): row base + 4b + i, token j
-  const int64_t v = base + 4 * b + kk;
-  const int t = lo;
-  unsigned long long key = 0;
-  if (t < kTok && v < vocab) {
-    const uint32_t bits = f64_to_bf16_bits(acc0 + acc1);
-    if (logits) logits[t * vocab + v] = (uint16_t)bits;
-    key = logit_key(bits, v);
-  }
-  // the wave's best key of token lo: lanes with equal lane & 3
+  // the wave's best key of token j: lanes with equal lane & 3
 #pragma unroll
   for (int off = 4; off < 64; off <<= 1) {
     const unsigned long long o = __shfl_xor(key, off, 64);
@@ -177,10 +210,13 @@ __global__ void __launch_bounds__(64 * kMfmaWaves)
 template <int kTok>
 int launch_mfma(const uint16_t* w, const uint16_t* h, int64_t d, int64_t vocab, const int64_t* ids, uint16_t* logits,
                 int64_t* pred, int64_t* result, Workspace* ws, hipStream_t st) {
-  const int64_t rows = 16 * kMfmaWaves;
-  const unsigned nb = (unsigned)((vocab + rows - 1) / rows);
+  // every wave resident at once, each with a contiguous run of tiles
+  const int64_t ntile = (vocab + 3) / 4;
+  const int tpw = (int)((ntile + kMfmaResidentWaves - 1) / kMfmaResidentWaves);
+  const int64_t nw = (ntile + tpw - 1) / tpw;
+  const unsigned nb = (unsigned)((nw + kMfmaWaves - 1) / kMfmaWaves);
   const size_t lds = (size_t)4 * (size_t)d * 2;
-  hipLaunchKernelGGL((lm_head_mfma_kernel<kTok>), dim3(nb), dim3(64 * kMfmaWaves), lds, st, w, h, d, vocab, ids,
+  hipLaunchKernelGGL((lm_head_mfma_kernel<kTok>), dim3(nb), dim3(64 * kMfmaWaves), lds, st, w, h, d, vocab, tpw, ids,
                      logits, pred, result, ws);
   return check_launch("hsmoe_lm_head_accept");
 }

@@ -97,10 +97,14 @@ def test_router_ties_and_no_bias(dev):
     assert torch.allclose(w, torch.full_like(w, 0.25))
 
 
-@pytest.mark.parametrize("n_tok,vocab", [(1, 4096), (3, 129280), (8, 1000), (2, 70001), (4, 33333)])
-def test_lm_head_logits_argmax_bit_exact(dev, n_tok, vocab):
+@pytest.mark.parametrize(
+    "n_tok,vocab,d",
+    [(1, 4096, 512), (3, 129280, 4096), (8, 1000, 512), (2, 70001, 4096), (4, 33333, 4096),
+     # the MFMA form with one group per row, with groups that do not fill its load pipeline, and with fewer
+     # 4-row tiles than waves
+     (3, 3001, 512), (4, 20001, 1536), (2, 5, 1536)])
+def test_lm_head_logits_argmax_bit_exact(dev, n_tok, vocab, d):
     seed = 7 + n_tok
-    d = 4096 if vocab > 5000 else 512
     lm = synthetic.normal_bf16(seed, synthetic.tag(synthetic.KIND_LM_HEAD), (vocab, d), 0.0, 0.02, dev)
     h = synthetic.hidden(seed, 1, n_tok, d, dev)
     ids = torch.randint(0, vocab, (n_tok,), device=dev)
