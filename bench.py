@@ -426,7 +426,7 @@ def run_config2(torch, args, lb: LayerBench, cpu_info):
            "unique_experts_avg": u_avg, "accepted": acc, "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
            "roofline": roofline("moe_layer_kernel at M=3", layer_bytes, sl["median_us"],
                                 pmc_traffic("moe_layer_kernel_m3_pmc.json"),
-                                lm_head=roofline("lm_head_kernel + accept (T=3)", LM_HEAD_BYTES, sh["median_us"])),
+                                lm_head=roofline("lm_head_mfma_kernel + accept (T=3)", LM_HEAD_BYTES, sh["median_us"])),
            "cpu_baseline": None}
     if not args.no_cpu_baseline:
         from oracle import cpu_ref
