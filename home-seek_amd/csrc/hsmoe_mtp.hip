@@ -83,8 +83,10 @@ __device__ void accept_tail(const int64_t* __restrict__ ids, int64_t* __restrict
 // quarter of the columns; at the end of a row the 4 blocks' partials are
 // added across lanes.  HBM streams long contiguous runs per row best: 64
 // bytes per row and group over 16 rows ran at 4.15 TB/s, 128 bytes at 4.5,
-// 1 KB over 4 rows at 4.8.  Tiles are dealt to waves in contiguous runs
-// (tiles_per_wave), with the load pipeline running on across a wave's tiles.
+// 1 KB over 4 rows at 4.8.  Tiles are dealt to waves grid-stride (wave w
+// takes tiles w, w + waves, ...), so that the grid reads one contiguous
+// window of the head at a time (a contiguous run of tiles per wave was ~4%
+// slower), with the load pipeline running on across a wave's tiles.
 // The hidden states sit in LDS as bf16 [4][d]; a B lane reads the same
 // columns as its A lane in 16-byte LDS loads.  Products of bf16 values are
 // exact in fp64 and every partial sum is a subset sum of a row's products,
@@ -104,7 +106,7 @@ __device__ __forceinline__ double bf16_lane(const uint4& q, int n) {
 template <int kTok>
 __global__ void __launch_bounds__(64 * kMfmaWaves)
     lm_head_mfma_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ h, int64_t d, int64_t vocab,
-                        int tiles_per_wave, const int64_t* __restrict__ ids, uint16_t* __restrict__ logits,
+                        const int64_t* __restrict__ ids, uint16_t* __restrict__ logits,
                         int64_t* __restrict__ pred_out, int64_t* __restrict__ result_out,
                         Workspace* __restrict__ ws) {
   extern __shared__ uint16_t s_hb[];  // [4][d] bf16, rows >= kTok zero
@@ -119,10 +121,11 @@ __global__ void __launch_bounds__(64 * kMfmaWaves)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lo = lane & 3, slot = lane >> 2;  // A row i / B token j; (block, k) pair
   const int64_t ntile = (vocab + 3) / 4;
-  const int64_t t0 = ((int64_t)blockIdx.x * kMfmaWaves + wave) * tiles_per_wave;
-  const int64_t t1 = t0 + tiles_per_wave < ntile ? t0 + tiles_per_wave : ntile;
+  // tiles t0, t0 + nwv, t0 + 2 nwv, ...: at any moment the grid streams one contiguous window of the head
+  const int64_t t0 = (int64_t)blockIdx.x * kMfmaWaves + wave, nwv = (int64_t)gridDim.x * kMfmaWaves;
+  const int64_t ntw = t0 < ntile ? (ntile - 1 - t0) / nwv + 1 : 0;
   const int ng = (int)(d / kMfmaGroupCols);
-  const int64_t nf = t1 > t0 ? (t1 - t0) * ng : 0;  // (tile, group) steps of this wave
+  const int64_t nf = ntw * ng;  // (tile, group) steps of this wave
   const uint4* hq = reinterpret_cast<const uint4*>(s_hb + (int64_t)lo * d + 8 * slot);
   auto row_ptr = [&](int64_t t) {  // rows past the end read the last row; their sums are dropped
     const int64_t r = 4 * t + lo < vocab ? 4 * t + lo : vocab - 1;
@@ -139,7 +142,7 @@ __global__ void __launch_bounds__(64 * kMfmaWaves)
     for (int h2 = 0; h2 < kMfmaW; ++h2) q[p][h2] = p < nf ? lp[16 * (kMfmaW * lg + h2)] : make_uint4(0, 0, 0, 0);
     if (p < nf && ++lg == ng) {
       lg = 0;
-      lp = row_ptr(++lt);
+      lp = row_ptr(lt += nwv);
     }
   }
   double acc0 = 0.0, acc1 = 0.0;
@@ -163,7 +166,7 @@ __global__ void __launch_bounds__(64 * kMfmaWaves)
         }
         if (more && ++lg == ng) {
           lg = 0;
-          lp = row_ptr(++lt);
+          lp = row_ptr(lt += nwv);
         }
         if (++cg == ng) {
           // lane (i, b, j): block b's partial of row 4 ct + i, token j; add the 4 blocks
@@ -180,7 +183,7 @@ __global__ void __launch_bounds__(64 * kMfmaWaves)
           acc0 = 0.0;
           acc1 = 0.0;
           cg = 0;
-          ++ct;
+          ct += nwv;
         }
       }
     }
@@ -210,13 +213,12 @@ __global__ void __launch_bounds__(64 * kMfmaWaves)
 template <int kTok>
 int launch_mfma(const uint16_t* w, const uint16_t* h, int64_t d, int64_t vocab, const int64_t* ids, uint16_t* logits,
                 int64_t* pred, int64_t* result, Workspace* ws, hipStream_t st) {
-  // every wave resident at once, each with a contiguous run of tiles
+  // every wave resident at once (no more waves than tiles)
   const int64_t ntile = (vocab + 3) / 4;
-  const int tpw = (int)((ntile + kMfmaResidentWaves - 1) / kMfmaResidentWaves);
-  const int64_t nw = (ntile + tpw - 1) / tpw;
+  const int64_t nw = ntile < kMfmaResidentWaves ? ntile : kMfmaResidentWaves;
   const unsigned nb = (unsigned)((nw + kMfmaWaves - 1) / kMfmaWaves);
   const size_t lds = (size_t)4 * (size_t)d * 2;
-  hipLaunchKernelGGL((lm_head_mfma_kernel<kTok>), dim3(nb), dim3(64 * kMfmaWaves), lds, st, w, h, d, vocab, tpw, ids,
+  hipLaunchKernelGGL((lm_head_mfma_kernel<kTok>), dim3(nb), dim3(64 * kMfmaWaves), lds, st, w, h, d, vocab, ids,
                      logits, pred, result, ws);
   return check_launch("hsmoe_lm_head_accept");
 }
