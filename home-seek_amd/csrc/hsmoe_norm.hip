@@ -32,14 +32,33 @@ __global__ void __launch_bounds__(kThreads)
   const int chunks = (int)(d / 8);
   const int64_t base = (int64_t)blockIdx.x * chunks;
   float s = 0.0f;
-  for (int c = threadIdx.x; c < chunks; c += kThreads) {
-    uint4 v = x[base + c];
-    wrow[c] = w[c];
-    if (kAdd) v = norm_add_chunk(v, add[base + c]);
-    if (kRes) v = norm_add_chunk(v, res[c]);
-    if (h_out) h_out[base + c] = v;
-    row[c] = v;
-    s = norm_sumsq_chunk(v, s);
+  // every load of kB chunks in flight at once (one memory round trip for d <= 8192), then the chunks in column order
+  constexpr int kB = 4;
+  for (int c0 = threadIdx.x; c0 < chunks; c0 += kB * kThreads) {
+    uint4 v[kB], a[kB], r[kB], wv[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const int c = c0 + b * kThreads;
+      if (c < chunks) {
+        v[b] = x[base + c];
+        wv[b] = w[c];
+        if (kAdd) a[b] = add[base + c];
+        if (kRes) r[b] = res[c];
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const int c = c0 + b * kThreads;
+      if (c < chunks) {
+        uint4 u = v[b];
+        wrow[c] = wv[b];
+        if (kAdd) u = norm_add_chunk(u, a[b]);
+        if (kRes) u = norm_add_chunk(u, r[b]);
+        if (h_out) h_out[base + c] = u;
+        row[c] = u;
+        s = norm_sumsq_chunk(u, s);
+      }
+    }
   }
   s = norm_wave_sum(s);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
