@@ -227,14 +227,14 @@ extern __shared__ double s_h[];  // [kTok][d] when kLds
 
 template <int kTok, bool kLds>
 __global__ void __launch_bounds__(64 * kWaves)
-    lm_head_kernel(const uint16_t* __restrict__ w, const double* __restrict__ h64g, int64_t d, int64_t vocab,
-                   const int64_t* __restrict__ ids, uint16_t* __restrict__ logits, int64_t* __restrict__ pred_out,
-                   int64_t* __restrict__ result_out, Workspace* __restrict__ ws) {
+    lm_head_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ hb, const double* __restrict__ h64g,
+                   int64_t d, int64_t vocab, const int64_t* __restrict__ ids, uint16_t* __restrict__ logits,
+                   int64_t* __restrict__ pred_out, int64_t* __restrict__ result_out, Workspace* __restrict__ ws) {
   __shared__ unsigned long long s_key[kWaves][kTok];
   __shared__ int s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if constexpr (kLds) {
-    for (int64_t c = threadIdx.x; c < kTok * d; c += 64 * kWaves) s_h[c] = h64g[c];
+  if constexpr (kLds) {  // the bf16 hidden states widened to fp64 on their way into LDS
+    for (int64_t c = threadIdx.x; c < kTok * d; c += 64 * kWaves) s_h[c] = (double)bf16_bits_to_f32(hb[c]);
     __syncthreads();
   }
   const double* __restrict__ h64 = kLds ? s_h : h64g;
@@ -315,9 +315,11 @@ __global__ void __launch_bounds__(64 * kWaves)
   accept_tail<kTok>(ids, pred_out, result_out, ws);
 }
 
+// h: bf16 [kTok][d]; h64: workspace for their fp64 copy, used (and filled by
+// widen_h_kernel) only when they do not fit in LDS.
 template <int kTok>
-int launch(const uint16_t* w, const double* h64, int64_t d, int64_t vocab, const int64_t* ids, uint16_t* logits,
-           int64_t* pred, int64_t* result, Workspace* ws, hipStream_t st) {
+int launch(const uint16_t* w, const uint16_t* h, double* h64, int64_t d, int64_t vocab, const int64_t* ids,
+           uint16_t* logits, int64_t* pred, int64_t* result, Workspace* ws, hipStream_t st) {
   const unsigned nb = (unsigned)((vocab + kRowsPerBlock - 1) / kRowsPerBlock);
   const size_t lds = (size_t)kTok * (size_t)d * 8;
   if (lds <= kLdsHBytes) {
@@ -328,10 +330,13 @@ int launch(const uint16_t* w, const double* h64, int64_t d, int64_t vocab, const
         return fail(HSMOE_ERR_LAUNCH, "hsmoe_lm_head_accept: could not allow %zu bytes of LDS", kLdsHBytes);
       raised = true;
     }
-    hipLaunchKernelGGL((lm_head_kernel<kTok, true>), dim3(nb), dim3(64 * kWaves), lds, st, w, h64, d, vocab, ids,
+    hipLaunchKernelGGL((lm_head_kernel<kTok, true>), dim3(nb), dim3(64 * kWaves), lds, st, w, h, h64, d, vocab, ids,
                        logits, pred, result, ws);
   } else {
-    hipLaunchKernelGGL((lm_head_kernel<kTok, false>), dim3(nb), dim3(64 * kWaves), 0, st, w, h64, d, vocab, ids,
+    hipLaunchKernelGGL(widen_h_kernel, dim3((unsigned)((kTok * d + 255) / 256)), dim3(256), 0, st, h, kTok * d, h64);
+    const int rc = check_launch("hsmoe_lm_head_accept(widen)");
+    if (rc) return rc;
+    hipLaunchKernelGGL((lm_head_kernel<kTok, false>), dim3(nb), dim3(64 * kWaves), 0, st, w, h, h64, d, vocab, ids,
                        logits, pred, result, ws);
   }
   return check_launch("hsmoe_lm_head_accept");
@@ -375,18 +380,15 @@ extern "C" int hsmoe_lm_head_accept(const void* h, const void* lm_head, int64_t 
     }
   }
   double* h64 = (double*)((char*)workspace + h64_offset());
-  hipLaunchKernelGGL(widen_h_kernel, dim3((unsigned)((n_tok * d + 255) / 256)), dim3(256), 0, st, (const uint16_t*)h,
-                     n_tok * d, h64);
-  int rc = check_launch("hsmoe_lm_head_accept(widen)");
-  if (rc) return rc;
+  const uint16_t* hb = (const uint16_t*)h;
   switch (n_tok) {
-    case 1: return launch<1>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
-    case 2: return launch<2>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
-    case 3: return launch<3>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
-    case 4: return launch<4>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
-    case 5: return launch<5>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
-    case 6: return launch<6>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
-    case 7: return launch<7>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
-    default: return launch<8>(w, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 1: return launch<1>(w, hb, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 2: return launch<2>(w, hb, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 3: return launch<3>(w, hb, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 4: return launch<4>(w, hb, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 5: return launch<5>(w, hb, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 6: return launch<6>(w, hb, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    case 7: return launch<7>(w, hb, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    default: return launch<8>(w, hb, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
   }
 }

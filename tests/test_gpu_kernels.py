@@ -102,7 +102,9 @@ def test_router_ties_and_no_bias(dev):
     [(1, 4096, 512), (3, 129280, 4096), (8, 1000, 512), (2, 70001, 4096), (4, 33333, 4096),
      # the MFMA form with one group per row, with groups that do not fill its load pipeline, and with fewer
      # 4-row tiles than waves
-     (3, 3001, 512), (4, 20001, 1536), (2, 5, 1536)])
+     (3, 3001, 512), (4, 20001, 1536), (2, 5, 1536),
+     # six tokens of 4096: fp64 hidden states past the LDS budget, widened into the workspace by a launch of their own
+     (6, 3001, 4096)])
 def test_lm_head_logits_argmax_bit_exact(dev, n_tok, vocab, d):
     seed = 7 + n_tok
     lm = synthetic.normal_bf16(seed, synthetic.tag(synthetic.KIND_LM_HEAD), (vocab, d), 0.0, 0.02, dev)
