@@ -1,6 +1,7 @@
 // Routed-expert SwiGLU FFN for many tokens (prefill): a grouped GEMM over the
 // experts the tokens select, each expert's weights streamed from HBM once per
-// chunk of up to 32 of its tokens.
+// chunk of its tokens (gate/up: up to 32, or 64 for an expert with more than
+// 32; down: up to 32).
 //
 // Restates FusedMoEFFN._forward_legacy at B > 8 and the FP4 grouped route of
 // fused_expert_ffn_triton (fused_moe.py:269-380, 458-551) plus the shared
@@ -17,14 +18,17 @@
 // Launches (no host synchronisation):
 //   group    workgroup e buckets the pairs (t, j) routed to expert e, in (t, j)
 //            order (stable, deterministic); one more workgroup places the
-//            shared expert's M pairs.  Each bucket is cut into chunks of <= 32
-//            pairs.
+//            shared expert's M pairs.  Each bucket is cut into gate/up chunks
+//            (<= 32 pairs, or <= 64 for a bucket of more than 32, those first)
+//            and into down chunks of <= 32 pairs.
 //   gate_up  grid (chunk, 64-row block of I), one launch for the routed
 //            experts and one for the shared expert: wave w takes rows
 //            +16w..+16 of W1 and W3 over all of D in K-chunks of 256 columns.
 //            While chunk kc is multiplied, the token tile of kc+1 is in flight
 //            to registers (then LDS) and the weights of kc+2 to a third
-//            register buffer.  Writes the weighted activation (hi, lo).
+//            register buffer (a 64-pair chunk: no weights ahead, for the
+//            registers of its four token tiles).  Writes the weighted
+//            activation (hi, lo).
 //   down     grid (chunk, 128-row block of D), same pipeline over W2 (32 rows
 //            per wave) with the activation tile (hi and lo planes); writes one
 //            fp32 partial row per pair (no atomics).
@@ -42,6 +46,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kChunk = 32;        // tokens per chunk (two 16-token MFMA tiles)
+constexpr int kBigChunk = 64;     // tokens per chunk of an expert with more than kChunk pairs
 constexpr int kGuRT = 1;          // 16-row tiles per wave, gate/up (W1 and W3)
 constexpr int kDnRT = 2;          // 16-row tiles per wave, down (W2)
 constexpr int kGuRows = 64 * kGuRT;  // weight rows per workgroup
@@ -52,8 +57,9 @@ constexpr int kMaxPairs = 12288;  // m * top_k per call (LDS of the group kernel
 constexpr int kMaxExperts = 1024;
 
 struct Header {
-  int n_routed_chunks;  // chunks of routed experts; the shared expert's follow
+  int n_routed_chunks;  // gate/up chunks of routed experts (big experts' first); the shared expert's follow
   int n_pairs;
+  int n_dn_chunks;      // down chunks of routed experts (kChunk pairs each); the shared expert's follow
 };
 
 struct PrefillParams {
@@ -69,6 +75,9 @@ struct PrefillParams {
   int* chunk_e;            // [max_chunks] expert (n_experts = shared)
   int* chunk_p0;           // [max_chunks] first pair
   int* chunk_n;            // [max_chunks] pairs in the chunk
+  int* dn_e;               // [max_chunks] down chunks: every expert's pairs in chunks of kChunk
+  int* dn_p0;
+  int* dn_n;
   uint16_t* act_hi;        // bf16 [max_pairs][i]
   uint16_t* act_lo;        // bf16 [max_pairs][i]
   float* part;             // fp32 [max_pairs][d]
@@ -81,6 +90,13 @@ struct PrefillParams {
 };
 
 // ---------------------------------------------------------------- group
+// Pairs per gate/up chunk of an expert with cnt pairs: an expert with more
+// than kChunk pairs is cut into chunks of kBigChunk, so that its W1 and W3
+// are streamed half as often; big experts' chunks come first, so that the
+// longer workgroups start first.  The down pass keeps chunks of kChunk (its
+// token tile's size), in expert order: a second list.
+__device__ __forceinline__ int chunk_size(int cnt) { return cnt > kChunk ? kBigChunk : kChunk; }
+
 // Sum over the block of v (every thread passes its own value).
 __device__ __forceinline__ int block_sum(int v, int* s_red) {
 #pragma unroll
@@ -117,16 +133,19 @@ __global__ void __launch_bounds__(kThreads) prefill_group_kernel(PrefillParams p
   }
   __syncthreads();
   if (me == E) {
-    int pairs = 0, chunks = 0;
+    int pairs = 0, chunks = 0, dchunks = 0;
     for (int e = threadIdx.x; e < E; e += kThreads) {
       pairs += s_cnt[e];
-      chunks += (s_cnt[e] + kChunk - 1) / kChunk;
+      chunks += (s_cnt[e] + chunk_size(s_cnt[e]) - 1) / chunk_size(s_cnt[e]);
+      dchunks += (s_cnt[e] + kChunk - 1) / kChunk;
     }
     pairs = block_sum(pairs, s_red);
     chunks = block_sum(chunks, s_red);
+    dchunks = block_sum(dchunks, s_red);
     if (threadIdx.x == 0) {
       p.hdr->n_pairs = pairs + (p.shared ? p.m : 0);
       p.hdr->n_routed_chunks = chunks;
+      p.hdr->n_dn_chunks = dchunks;
     }
     for (int q = threadIdx.x; q < P; q += kThreads)
       if (s_e[q] < 0) p.pidx[(q / K) * (K + 1) + q % K] = -1;
@@ -137,23 +156,30 @@ __global__ void __launch_bounds__(kThreads) prefill_group_kernel(PrefillParams p
       p.pair_tok[pos] = t;
       p.pair_w[pos] = 1.0f;
       if (t % kChunk == 0) {
-        const int ch = chunks + t / kChunk;
-        p.chunk_e[ch] = E;
-        p.chunk_p0[ch] = pos;
-        p.chunk_n[ch] = min(kChunk, p.m - t);
+        const int ch = chunks + t / kChunk, dch = dchunks + t / kChunk;
+        p.chunk_e[ch] = p.dn_e[dch] = E;
+        p.chunk_p0[ch] = p.dn_p0[dch] = pos;
+        p.chunk_n[ch] = p.dn_n[dch] = min(kChunk, p.m - t);
       }
     }
     return;
   }
   const int cnt = s_cnt[me];
   if (cnt == 0) return;  // uniform across the workgroup
-  int off = 0, choff = 0;
-  for (int e = threadIdx.x; e < me; e += kThreads) {
-    off += s_cnt[e];
-    choff += (s_cnt[e] + kChunk - 1) / kChunk;
+  // chunks: the big experts' (expert order), then one per small expert (expert order)
+  const bool big = cnt > kChunk;
+  int off = 0, choff = 0, dnoff = 0;
+  for (int e = threadIdx.x; e < E; e += kThreads) {
+    const int c = s_cnt[e];
+    if (e < me) off += c;
+    if (e < me) dnoff += (c + kChunk - 1) / kChunk;
+    if (c > kChunk && (!big || e < me)) choff += (c + kBigChunk - 1) / kBigChunk;  // every big expert's chunks first
+    else if (!big && e < me && c > 0) ++choff;
   }
   off = block_sum(off, s_red);
   choff = block_sum(choff, s_red);
+  dnoff = block_sum(dnoff, s_red);
+  const int cs = chunk_size(cnt);
   int base = off;
   for (int q0 = 0; q0 < P; q0 += kThreads) {
     const int q = q0 + threadIdx.x;
@@ -176,10 +202,15 @@ __global__ void __launch_bounds__(kThreads) prefill_group_kernel(PrefillParams p
     base += total;
     __syncthreads();
   }
-  for (int c = threadIdx.x; c * kChunk < cnt; c += kThreads) {
+  for (int c = threadIdx.x; c * cs < cnt; c += kThreads) {
     p.chunk_e[choff + c] = me;
-    p.chunk_p0[choff + c] = off + c * kChunk;
-    p.chunk_n[choff + c] = min(kChunk, cnt - c * kChunk);
+    p.chunk_p0[choff + c] = off + c * cs;
+    p.chunk_n[choff + c] = min(cs, cnt - c * cs);
+  }
+  for (int c = threadIdx.x; c * kChunk < cnt; c += kThreads) {
+    p.dn_e[dnoff + c] = me;
+    p.dn_p0[dnoff + c] = off + c * kChunk;
+    p.dn_n[dnoff + c] = min(kChunk, cnt - c * kChunk);
   }
 }
 
@@ -194,29 +225,30 @@ struct Chunk {
   const uint64_t* ent;
 };
 
-// Chunk q of the routed experts (kShared = false) or of the shared expert.
-template <bool kShared>
+// Chunk q of the routed experts (kShared = false) or of the shared expert,
+// from the gate/up list or (kDown) the down list.
+template <bool kShared, bool kDown>
 __device__ __forceinline__ bool load_chunk(const PrefillParams& p, int q, Chunk& ch) {
-  const int nr = p.hdr->n_routed_chunks;
+  const int nr = kDown ? p.hdr->n_dn_chunks : p.hdr->n_routed_chunks;
   if (kShared) {
     if (q * kChunk >= p.m) return false;
     q += nr;
   } else if (q >= nr) {
     return false;
   }
-  ch.e = p.chunk_e[q];
-  ch.p0 = p.chunk_p0[q];
-  ch.n = p.chunk_n[q];
+  ch.e = kDown ? p.dn_e[q] : p.chunk_e[q];
+  ch.p0 = kDown ? p.dn_p0[q] : p.chunk_p0[q];
+  ch.n = kDown ? p.dn_n[q] : p.chunk_n[q];
   ch.ent = kShared ? p.shared : p.table + (int64_t)ch.e * 6;
   return true;
 }
 
-// This thread's share of a token tile [kChunk][kCols] of kPlanes planes,
+// This thread's share of a token tile [kC][kCols] of kPlanes planes,
 // held in registers between its global loads and its LDS store.  Rows past
 // the chunk's n tokens are zero and never loaded.
-template <int kPlanes>
+template <int kPlanes, int kC>
 struct XStage {
-  static constexpr int kPer = kChunk * kCols / 8 / kThreads;  // uint4 per thread and plane
+  static constexpr int kPer = kC * kCols / 8 / kThreads;  // uint4 per thread and plane
   uint4 v[kPlanes][kPer];
   template <typename Src>
   __device__ __forceinline__ void load(Src& src, int kc, int n) {
@@ -234,7 +266,7 @@ struct XStage {
 #pragma unroll
       for (int u = 0; u < kPer; ++u) {
         const int q = threadIdx.x + u * kThreads, tt = q / (kCols / 8), cc = q % (kCols / 8);
-        *reinterpret_cast<uint4*>(lds + pl * kChunk * (kCols + kPad) + tt * (kCols + kPad) + cc * 8) = v[pl][u];
+        *reinterpret_cast<uint4*>(lds + pl * kC * (kCols + kPad) + tt * (kCols + kPad) + cc * 8) = v[pl][u];
       }
   }
 };
@@ -257,7 +289,10 @@ struct WBuf {
 // tile of kc + 1 is in flight to registers and the weights of kc + 2 to the
 // third weight buffer; the tile loads are issued before the weight loads.
 // Buffers rotate statically (three steps per loop turn).
-template <int F, int kMats, int kRT, int kPlanes, typename Src, typename Mul>
+// kC: token tile rows; kBufs: weight buffers (3: the weights of kc + 2 in
+// flight, 2: those of kc + 1, 1: none ahead, for the larger token tile's
+// register budget).
+template <int F, int kMats, int kRT, int kPlanes, int kC, int kBufs, typename Src, typename Mul>
 __device__ __forceinline__ void pipeline(const uint64_t* ent, int w_slot, int n_rows, int row, int k, int g, int n,
                                          uint16_t* lds, Src&& src, Mul&& mul) {
   using W = WBuf<F, kMats, kRT>;
@@ -265,10 +300,11 @@ __device__ __forceinline__ void pipeline(const uint64_t* ent, int w_slot, int n_
   Mat mats[kMats];
 #pragma unroll
   for (int q = 0; q < kMats; ++q) mats[q] = make_mat<F>(ent[w_slot + 2 * q], ent[w_slot + 2 * q + 1], n_rows, k);
-  XStage<kPlanes> xr;
-  if constexpr (F == kBf16) {
-    // bf16 weights (a compatibility format, 4x the bytes): one buffer, no
-    // weight prefetch, so that this path never raises the kernel's registers
+  XStage<kPlanes, kC> xr;
+  if constexpr (F == kBf16 || kBufs == 1) {
+    // bf16 weights (a compatibility format, 4x the bytes), or one buffer
+    // asked for: no weight prefetch, so that this path never raises the
+    // kernel's registers
     W w;
     for (int kc = 0; kc < nkc; ++kc) {
       xr.load(src, kc, n);
@@ -277,6 +313,26 @@ __device__ __forceinline__ void pipeline(const uint64_t* ent, int w_slot, int n_
       xr.store(lds);
       __syncthreads();
       mul(w);
+    }
+    return;
+  }
+  if constexpr (kBufs == 2) {
+    W w0, w1;
+    xr.load(src, 0, n);
+    w0.load(mats, row, k, 0, g);
+    auto step2 = [&](const W& wc, W& wl, int kc) {
+      __syncthreads();
+      xr.store(lds);
+      __syncthreads();
+      if (kc + 1 < nkc) {
+        xr.load(src, kc + 1, n);
+        wl.load(mats, row, k, kc + 1, g);
+      }
+      mul(wc);
+    };
+    for (int kc = 0; kc < nkc; kc += 2) {
+      step2(w0, w1, kc);
+      if (kc + 1 < nkc) step2(w1, w0, kc + 1);
     }
     return;
   }
@@ -302,18 +358,19 @@ __device__ __forceinline__ void pipeline(const uint64_t* ent, int w_slot, int n_
 // ---------------------------------------------------------------- gate / up
 // Wave rows r0 .. r0+16*kGuRT-1 of W1 and W3 against the chunk's tokens; lane
 // (r, g) ends holding rows r0 + 16 rt + 4g + q of token tile*16 + r.
-template <int F>
+template <int F, int kC, int kBufs>
 __device__ void gate_up_chunk(const PrefillParams& p, const Chunk& ch, int r0, uint16_t* xs, const int* s_tok) {
   using W = WBuf<F, 2, kGuRT>;
+  constexpr int kTiles = kC / 16;
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int ntile = (ch.n + 15) / 16;
-  f32x4 ag[kGuRT][2], au[kGuRT][2];
+  f32x4 ag[kGuRT][kTiles], au[kGuRT][kTiles];
 #pragma unroll
   for (int rt = 0; rt < kGuRT; ++rt)
 #pragma unroll
-    for (int t = 0; t < 2; ++t) ag[rt][t] = au[rt][t] = f32x4{0, 0, 0, 0};
+    for (int t = 0; t < kTiles; ++t) ag[rt][t] = au[rt][t] = f32x4{0, 0, 0, 0};
   auto src = [&](int, int tt) { return p.x + (int64_t)s_tok[tt] * p.d; };
-  pipeline<F, 2, kGuRT, 1>(ch.ent, 0, p.i, r0 + r, p.d, g, ch.n, xs, src, [&](const W& w) {
+  pipeline<F, 2, kGuRT, 1, kC, kBufs>(ch.ent, 0, p.i, r0 + r, p.d, g, ch.n, xs, src, [&](const W& w) {
 #pragma unroll
     for (int b = 0; b < W::kSteps; ++b) {
 #pragma unroll
@@ -322,7 +379,7 @@ __device__ void gate_up_chunk(const PrefillParams& p, const Chunk& ch, int r0, u
         for (int rt = 0; rt < kGuRT; ++rt) {
           const bf16x8 f1 = w.b[0][rt].frag(b, j, g), f3 = w.b[1][rt].frag(b, j, g);
 #pragma unroll
-          for (int tile = 0; tile < 2; ++tile) {
+          for (int tile = 0; tile < kTiles; ++tile) {
             if (tile >= ntile) break;
             const bf16x8 xf = tile_frag(xs, kCols, tile, r, g, b, j);
             ag[rt][tile] = mfma16x16x32(f1, xf, ag[rt][tile]);
@@ -333,7 +390,7 @@ __device__ void gate_up_chunk(const PrefillParams& p, const Chunk& ch, int r0, u
     }
   });
 #pragma unroll
-  for (int tile = 0; tile < 2; ++tile) {
+  for (int tile = 0; tile < kTiles; ++tile) {
     const int tt = tile * 16 + r;
     if (tile >= ntile || tt >= ch.n) continue;
     const int64_t pr = ch.p0 + tt;
@@ -359,16 +416,28 @@ __device__ void gate_up_chunk(const PrefillParams& p, const Chunk& ch, int r0, u
 template <int F, bool kShared>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(F == kFp8Block ? 2 : 4)))
 prefill_gate_up_kernel(PrefillParams p) {
-  __shared__ __align__(16) uint16_t xs[kChunk * (kCols + kPad)];
-  __shared__ int s_tok[kChunk];
+  __shared__ __align__(16) uint16_t xs[kBigChunk * (kCols + kPad)];
+  __shared__ int s_tok[kBigChunk];
   const int nrb = p.i / kGuRows;
   Chunk ch;
-  if (!load_chunk<kShared>(p, blockIdx.x / nrb, ch)) return;
-  if (threadIdx.x < kChunk) s_tok[threadIdx.x] = threadIdx.x < ch.n ? p.pair_tok[ch.p0 + threadIdx.x] : 0;
+  if (!load_chunk<kShared, false>(p, blockIdx.x / nrb, ch)) return;
+  if (threadIdx.x < kBigChunk) s_tok[threadIdx.x] = threadIdx.x < ch.n ? p.pair_tok[ch.p0 + threadIdx.x] : 0;
   __syncthreads();
   const int r0 = (blockIdx.x % nrb) * kGuRows + 16 * kGuRT * (threadIdx.x >> 6);
-  if (ch.ent[1]) gate_up_chunk<F>(p, ch, r0, xs, s_tok);
-  else gate_up_chunk<kBf16>(p, ch, r0, xs, s_tok);
+  if (!kShared && ch.n > kChunk && ch.ent[1]) {  // a big expert's chunk (the shared expert's hold at most kChunk)
+    gate_up_chunk<F, kBigChunk, 1>(p, ch, r0, xs, s_tok);
+  } else if (ch.n > kChunk) {  // bf16 weights: the chunk as two kChunk halves (registers)
+    for (int h0 = 0; h0 < ch.n; h0 += kChunk) {
+      Chunk sub = ch;
+      sub.p0 = ch.p0 + h0;
+      sub.n = min(kChunk, ch.n - h0);
+      gate_up_chunk<kBf16, kChunk, 3>(p, sub, r0, xs, s_tok + h0);
+    }
+  } else if (ch.ent[1]) {
+    gate_up_chunk<F, kChunk, 3>(p, ch, r0, xs, s_tok);
+  } else {
+    gate_up_chunk<kBf16, kChunk, 3>(p, ch, r0, xs, s_tok);
+  }
 }
 
 // ---------------------------------------------------------------- down
@@ -382,7 +451,7 @@ __device__ void down_chunk(const PrefillParams& p, const Chunk& ch, int r0, uint
 #pragma unroll
   for (int rt = 0; rt < kDnRT; ++rt) acc[rt][0] = acc[rt][1] = f32x4{0, 0, 0, 0};
   auto src = [&](int pl, int tt) { return (pl ? p.act_lo : p.act_hi) + (int64_t)(ch.p0 + tt) * p.i; };
-  pipeline<F, 1, kDnRT, 2>(ch.ent, 4, p.d, r0 + r, p.i, g, ch.n, as, src, [&](const W& w) {
+  pipeline<F, 1, kDnRT, 2, kChunk, 3>(ch.ent, 4, p.d, r0 + r, p.i, g, ch.n, as, src, [&](const W& w) {
 #pragma unroll
     for (int b = 0; b < W::kSteps; ++b) {
 #pragma unroll
@@ -419,7 +488,7 @@ prefill_down_kernel(PrefillParams p) {
   __shared__ __align__(16) uint16_t as[2 * kChunk * (kCols + kPad)];  // hi plane, lo plane
   const int nrb = p.d / kDnRows;
   Chunk ch;
-  if (!load_chunk<kShared>(p, blockIdx.x / nrb, ch)) return;
+  if (!load_chunk<kShared, true>(p, blockIdx.x / nrb, ch)) return;
   const int r0 = (blockIdx.x % nrb) * kDnRows + 16 * kDnRT * (threadIdx.x >> 6);
   if (ch.ent[1]) down_chunk<F>(p, ch, r0, as);
   else down_chunk<kBf16>(p, ch, r0, as);
@@ -453,12 +522,13 @@ __global__ void __launch_bounds__(kThreads) prefill_combine_kernel(PrefillParams
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 struct Layout {
-  size_t hdr, pair_tok, pair_w, pidx, chunk_e, chunk_p0, chunk_n, act_hi, act_lo, part, total;
+  size_t hdr, pair_tok, pair_w, pidx, chunk_e, chunk_p0, chunk_n, dn_e, dn_p0, dn_n, act_hi, act_lo, part, total;
 };
 
 int64_t max_pairs(int64_t m, int top_k) { return m * top_k + m; }
-// Chunks of the routed experts: sum over experts of ceil(n_e / kChunk) <=
-// (experts with a pair) + (pairs) / kChunk.
+// Chunks of the routed experts in either list: at most sum over experts of
+// ceil(n_e / kChunk) <= (experts with a pair) + (pairs) / kChunk (a gate/up
+// chunk of kBigChunk covers two down chunks).
 int64_t max_routed_chunks(int64_t m, int64_t n_experts, int top_k) {
   const int64_t pk = m * top_k;
   return (n_experts < pk ? n_experts : pk) + (pk + kChunk - 1) / kChunk;
@@ -484,6 +554,12 @@ Layout layout(int64_t m, int64_t d, int64_t i, int64_t n_experts, int top_k) {
   L.chunk_p0 = o;
   o += align256((size_t)C * 4);
   L.chunk_n = o;
+  o += align256((size_t)C * 4);
+  L.dn_e = o;
+  o += align256((size_t)C * 4);
+  L.dn_p0 = o;
+  o += align256((size_t)C * 4);
+  L.dn_n = o;
   o += align256((size_t)C * 4);
   L.act_hi = o;
   o += align256((size_t)P * i * 2);
@@ -541,6 +617,9 @@ extern "C" int hsmoe_moe_prefill(const void* x, int64_t m, int64_t d, int64_t i,
   p.chunk_e = (int*)(ws + L.chunk_e);
   p.chunk_p0 = (int*)(ws + L.chunk_p0);
   p.chunk_n = (int*)(ws + L.chunk_n);
+  p.dn_e = (int*)(ws + L.dn_e);
+  p.dn_p0 = (int*)(ws + L.dn_p0);
+  p.dn_n = (int*)(ws + L.dn_n);
   p.act_hi = (uint16_t*)(ws + L.act_hi);
   p.act_lo = (uint16_t*)(ws + L.act_lo);
   p.part = (float*)(ws + L.part);
