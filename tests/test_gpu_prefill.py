@@ -79,7 +79,8 @@ def test_small_zipf_routing_matches_oracle(small, dev, m):
 
 
 def test_hot_expert_spans_many_chunks(small, dev):
-    """One expert chosen by all 100 tokens (4 chunks of <= 32), in varying slots."""
+    """One expert chosen by all 100 tokens (gate/up: chunks of 64 + 36 pairs; down: 4 chunks of <= 32), in varying
+    slots."""
     m = 100
     x = synthetic.hidden(SEED, 3, m, small.d, dev)
     idx, w = synthetic.zipf_routing(SEED, m, small.E, K)
@@ -91,6 +92,25 @@ def test_hot_expert_spans_many_chunks(small, dev):
     out, f32 = run(small, x, idx, w, shared=False)
     ref = small.oracle(x, idx, w, shared=False)
     check_close(f32.cpu().numpy(), orc.to_np_bf16(out), ref, "hot expert")
+
+
+def test_chunk_size_boundaries(small, dev):
+    """Buckets of 32, 33, 64, 65 and 97 pairs: gate/up chunks of 32 | 33 | 64 | 64 + 1 | 64 + 33 pairs (the
+    64-pair form past 32), down chunks of at most 32; the five experts fill the first slots of their tokens."""
+    sizes = {3: 32, 5: 33, 11: 64, 17: 65, 23: 97}
+    m = max(sizes.values())
+    x = synthetic.hidden(SEED, 7, m, small.d, dev)
+    idx, w = synthetic.zipf_routing(SEED + 7, m, small.E, K)
+    for t in range(m):
+        heads = [e for e in sorted(sizes, key=sizes.get) if t < sizes[e]][:K]
+        rest = [int(e) for e in idx[t] if e not in sizes]
+        rest += [e for e in range(small.E) if e not in sizes and e not in rest][:K]
+        idx[t] = (heads + rest)[:K]
+    counts = np.bincount(idx.reshape(-1), minlength=small.E)
+    assert all(counts[e] == n for e, n in sizes.items())
+    out, f32 = run(small, x, idx, w, shared=False)
+    ref = small.oracle(x, idx, w, shared=False)
+    check_close(f32.cpu().numpy(), orc.to_np_bf16(out), ref, "chunk boundaries")
 
 
 def test_invalid_ids_absent_experts_and_empty_tokens(small, dev):
@@ -132,13 +152,18 @@ def test_matches_decode_kernels_and_is_deterministic(small, dev):
 
 def test_fused_moe_forward_with_fp32_scales_and_bf16_experts(small, dev):
     """FusedMoEFFN.forward at B > 8 with the reference's loader shapes: fp32
-    scales, 3-tuple bf16 weights and None."""
-    m = 24
+    scales, 3-tuple bf16 weights and None; one bf16 expert is chosen by all 40
+    tokens (its gate/up chunk of 40 pairs taken as two halves of <= 32)."""
+    m = 40
     moe = fused_moe.FusedMoEFFN(small.E, small.i, small.d, 10.0)
     x = synthetic.hidden(SEED, 6, m, small.d, dev)
     idx, w = synthetic.zipf_routing(SEED + 6, m, small.E, K)
     ids = sorted({int(e) for e in idx.reshape(-1)})
     absent, as_bf16 = ids[0], set(ids[1:4])
+    hot = ids[1]
+    for t in range(m):
+        if hot not in idx[t]:
+            idx[t, t % K] = hot
 
     def loader(layer_idx, eid):
         if eid == absent:
