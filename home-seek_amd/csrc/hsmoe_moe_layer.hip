@@ -786,7 +786,10 @@ __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg
       for (int c = 0; c < 4; ++c) acc[c] = __fadd_rn(acc[c], xr[(wave * 64 + lane) * 4 + c]);
     }
   } else {
-    if (fmt == kFp4E8M0) down_any<kFp4E8M0, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
+    // FP4 E8M0 at m >= 3: batches of 8 steps instead of 16 (measured at M=3:
+    // 78.0 us against 78.8; at M=1 the 16-step batch is 0.2 us faster)
+    if (fmt == kFp4E8M0 && m >= 3) down_any<kFp4E8M0, true, 8>(ent, g_tile, m, i, p.d, r0, 0, i / 128, acc, stage);
+    else if (fmt == kFp4E8M0) down_any<kFp4E8M0, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
     else if (fmt == kFp4F32) down_any<kFp4F32, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
     else down_any<kBf16, true>(ent, g_tile, m, i, p.d, r0, acc, stage);
   }

@@ -311,10 +311,11 @@ __device__ __forceinline__ void down_rows(const uint64_t* ent, const uint16_t* a
   }
 }
 
-template <int F, bool kDeep, typename Ready>
+// kCap: the largest batch instantiated (steps loaded per round).
+template <int F, bool kDeep, int kCap = 64, typename Ready>
 __device__ __forceinline__ void down_any(const uint64_t* ent, const uint16_t* as, int m, int i, int d, int r0,
                                          int st0, int st1, f32x4& acc, Ready&& ready) {
-  constexpr int kMax = down_batch<F, kDeep>();
+  constexpr int kMax = down_batch<F, kDeep>() < kCap ? down_batch<F, kDeep>() : kCap;
   const int b = batch_for<kMax>(st1 - st0);
   if (b == kMax) down_rows<F, kMax>(ent, as, m, i, d, r0, st0, st1, acc, ready);
   else if (kMax > 8 && b == 8) down_rows<F, (kMax > 8 ? 8 : 1)>(ent, as, m, i, d, r0, st0, st1, acc, ready);
