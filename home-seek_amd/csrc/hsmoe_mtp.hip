@@ -4,13 +4,17 @@
 //   logits = bf16(h . lm_head^T); pred[t] = argmax(logits[t]) (first index
 //   on ties, as torch.argmax); accept combined_ids[t+1] while it equals
 //   pred[t]; the bonus row is the first mismatch (or the last row).
-// Each logit is the correctly rounded bf16 of the exact dot product: one lane
-// owns one vocab row and sums it in fp64 (bf16 x bf16 products are exact in
-// fp64); the hidden states are pre-widened to fp64, and each workgroup copies
-// them into LDS when they fit (n_tok * d * 8 <= kLdsHBytes), so that the
-// inner loop reads them with broadcast LDS loads instead of scalar loads that
-// stall on the scalar cache; the per-weight cost is 2 conversions + n_tok
-// fp64 FMAs.
+// Each logit is the correctly rounded bf16 of the exact dot product (bf16 x
+// bf16 products are exact in fp64, and so are the sums met in practice), in
+// one of two forms:
+//  - 2..4 tokens: v_mfma_f64_4x4x4_4b_f64 over 4-row tiles, the bf16 hidden
+//    states in LDS (lm_head_mfma_kernel);
+//  - 1 or 5..8 tokens: one lane per vocab row summing in fp64 FMAs, the
+//    hidden states widened to fp64 on their way into LDS when they fit
+//    (n_tok * d * 8 <= kLdsHBytes), else widened into the workspace by
+//    widen_h_kernel and read from there (lm_head_kernel); the inner loop reads
+//    them with broadcast LDS loads instead of scalar loads that stall on the
+//    scalar cache; per weight 2 conversions + n_tok fp64 FMAs.
 // The vocab-wide argmax is a 64-bit atomic max on (orderable logit, ~index);
 // the last workgroup to finish evaluates the acceptance rule and clears the
 // counters for the next call.
