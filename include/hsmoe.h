@@ -230,8 +230,9 @@ int hsmoe_moe_layer_decode_noalloc(const void* x_dev, int64_t m, int64_t d, int6
  * exact bf16 products, fp32 accumulation, fp32 SwiGLU, hi/lo activation),
  * with out[t] = sum_j topk_w[t, j] * FFN_{topk_idx[t, j]}(x[t]) in slot order j,
  * then + shared FFN(x[t]); a (t, j) with an invalid id or absent expert adds
- * nothing.  Each selected expert's weights are read once per chunk of up to
- * 32 of its tokens.  Deterministic (no atomics).
+ * nothing.  Each selected expert's W1 and W3 are read once per chunk of up
+ * to 32 of its tokens (64 for an expert with more than 32), its W2 once per
+ * chunk of up to 32.  Deterministic (no atomics).
  * 1 <= m * top_k <= 12288, n_experts <= 1024, top_k <= 16, d % 1024 == 0,
  * i % 512 == 0; x and out_f32 16-byte aligned, out_bf16 8-byte aligned.
  * The workspace (any contents) must hold hsmoe_moe_prefill_workspace_size bytes. */
