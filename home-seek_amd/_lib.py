@@ -15,6 +15,10 @@ LIB_PATH = Path(__file__).resolve().parent / "libhsmoe.so"
 
 SCALE_E8M0 = 0
 SCALE_F32 = 1
+DATA_FP4 = 0
+DATA_E4M3 = 1
+OUT_F32 = 0
+OUT_BF16 = 1
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -30,6 +34,8 @@ _SIGNATURES = {
     "hsmoe_clear_error": (None, []),
     "hsmoe_fp4_dequant_bf16": (_int, [_c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p]),
     "hsmoe_fp8_dequant_bf16": (_int, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
+    "hsmoe_dequant_blocked": (_int, [_c_void_p, _int, _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p, _int,
+                                     _c_void_p]),
     "hsmoe_router_workspace_size": (_size, [_i64, _i64]),
     "hsmoe_router_topk": (_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _int, _f32, _c_void_p, _c_void_p,
                                  _c_void_p, _c_void_p, _size, _c_void_p]),
@@ -60,6 +66,8 @@ _SIGNATURES = {
     "hsmoe_rms_norm": (_int, [_c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p, _c_void_p]),
     "hsmoe_add_rms_norm": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p,
                                   _c_void_p, _c_void_p]),
+    "hsmoe_xor_checksum_workspace_size": (_size, []),
+    "hsmoe_xor_checksum": (_int, [_c_void_p, _i64, _c_void_p, _c_void_p, _size, _c_void_p]),
     "hsmoe_gen_bytes": (_int, [_u64, _i64, _c_void_p, _c_void_p]),
     "hsmoe_gen_e4m3": (_int, [_u64, _i64, _c_void_p, _c_void_p]),
     "hsmoe_gen_e8m0": (_int, [_u64, _i64, _int, _int, _c_void_p, _c_void_p]),

@@ -109,15 +109,22 @@ def checkpoint_shape(index: CheckpointIndex) -> dict:
 
 
 def _e8m0_bytes(scale: torch.Tensor) -> torch.Tensor:
-    """E8M0 scale bytes: one-byte scales as they are; fp32 scales that are exact
-    powers of two (2^(e-127), e in 1..254) as their exponent byte."""
-    if scale.element_size() == 1:
+    """E8M0 scale bytes of an FP4 weight's scales.  float8_e8m0fnu scales are
+    their bytes.  Every other dtype is taken by value, as the reference's
+    loaders do (scale.to(torch.float32), engine.py:1066-1080,
+    weight_loader.py:40-44), so a uint8 or int8 scale of 127 means 127.0, not
+    2^0; those values are stored as their exponent byte when they are exact
+    positive powers of two (2^(e-127), e in 1..254), and refused otherwise:
+    the store holds E8M0 exponents only."""
+    if scale.dtype == torch.float8_e8m0fnu:
         return scale.view(torch.uint8)
     f = scale.to(torch.float32)
     bits = f.view(torch.int32)
     exp = (bits >> 23) & 0xFF
     if bool(((bits & 0x807FFFFF) != 0).any()) or bool(((exp == 0) | (exp == 255)).any()):
-        raise ValueError("fp32 FP4 scales must be positive powers of two to be stored as E8M0")
+        raise ValueError(f"FP4 scales of dtype {scale.dtype} are taken by value and must then be positive powers "
+                         "of two to be stored as E8M0 exponents (other scales: pass the weights as fp32-scale "
+                         "tuples to FusedMoEFFN.forward instead)")
     return exp.to(torch.uint8)
 
 
@@ -225,9 +232,22 @@ def load_layer_weights(index: CheckpointIndex, layer: int, device, prefix: str |
     return lw
 
 
+def select_lm_head(index: CheckpointIndex, config, embed, device):
+    """The lm_head as the reference picks it (engine.py:431-443): the embedding
+    when tie_word_embeddings is set and an embedding exists; else head.weight,
+    else output.weight, else the embedding (None when there is none)."""
+    if getattr(config, "tie_word_embeddings", False) and embed is not None:
+        return embed
+    for key in ("head", "output"):
+        w = _bf16_weight(index, f"{key}.weight", device, f"{key}.scale")
+        if w is not None:
+            return w
+    return embed
+
+
 def load_engine(weight_dir: str, config=None, device="cuda", with_mtp: bool = True, log=None):
     """A HomeSeekMoEEngine over a checkpoint: the expert store, the FFN layer
-    weights, embed / lm_head (head.weight, else the tied embedding) / final
+    weights, embed / lm_head (select_lm_head) / final
     norm, and the MTP block's FFN weights and norms when present."""
     from .engine import HomeSeekMoEEngine
     from .model_config import MoEConfig
@@ -239,7 +259,7 @@ def load_engine(weight_dir: str, config=None, device="cuda", with_mtp: bool = Tr
     store = load_expert_store(index, device, shape, with_mtp, log)
     lws = {l: load_layer_weights(index, l, device) for l in range(shape["n_layers"])}
     embed = _bf16_weight(index, "embed.weight", device)
-    head = _bf16_weight(index, "head.weight", device, "head.scale")
+    head = select_lm_head(index, config, embed, device)
     norm = _bf16_weight(index, "norm.weight", device)
     mtp = None
     if with_mtp and shape["mtp"]:
@@ -250,5 +270,5 @@ def load_engine(weight_dir: str, config=None, device="cuda", with_mtp: bool = Tr
             if w is not None:
                 mtp[f"{n}.weight"] = w
     index.close()
-    return HomeSeekMoEEngine(config, store, lws, lm_head=head if head is not None else embed, norm_weight=norm,
+    return HomeSeekMoEEngine(config, store, lws, lm_head=head, norm_weight=norm,
                              embed=embed, mtp_weights=mtp)

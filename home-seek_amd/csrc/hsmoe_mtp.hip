@@ -222,6 +222,14 @@ int launch_mfma(const uint16_t* w, const uint16_t* h, int64_t d, int64_t vocab, 
   const int64_t nw = ntile < kMfmaResidentWaves ? ntile : kMfmaResidentWaves;
   const unsigned nb = (unsigned)((nw + kMfmaWaves - 1) / kMfmaWaves);
   const size_t lds = (size_t)4 * (size_t)d * 2;
+  constexpr size_t kMaxLds = (size_t)4 * 8192 * 2;  // d <= 8192: 64 KiB of hidden states, beyond the default
+  static bool raised = false;                       // allow it once per instantiation
+  if (!raised) {
+    if (hipFuncSetAttribute((const void*)lm_head_mfma_kernel<kTok>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)kMaxLds) != hipSuccess)
+      return fail(HSMOE_ERR_LAUNCH, "hsmoe_lm_head_accept: could not allow %zu bytes of LDS", kMaxLds);
+    raised = true;
+  }
   hipLaunchKernelGGL((lm_head_mfma_kernel<kTok>), dim3(nb), dim3(64 * kMfmaWaves), lds, st, w, h, d, vocab, ids,
                      logits, pred, result, ws);
   return check_launch("hsmoe_lm_head_accept");

@@ -165,7 +165,8 @@ class HomeSeekMoEEngine:
                 and input_ids.dtype == torch.int64):
             # hash ids (tid2eid[input_ids], weight 1/k, engine.py:1018-1023) looked up
             # inside the one-launch layer kernel (hsmoe_moe_layer_decode_routed)
-            ids = input_ids.reshape(-1)
+            # a copy: a caller may rewrite its id buffer in place (GreedyDecoder does)
+            ids = input_ids.reshape(-1).clone()
             out, _ = ops.moe_layer_decode_routed(
                 flat, tid2eid, table, SCALE_E8M0, self.store.shared_entry(layer_idx),
                 self.config.moe_intermediate_size, weight_all=1.0 / k, token_ids=ids, top_k=k,
@@ -219,6 +220,7 @@ class HomeSeekMoEEngine:
             words = [w.to(torch.int64) for w in ops.moe_layer_status_words(self.device)]
             vals = torch.cat([result] + words).tolist()
             if any(vals[2:]):
+                ops.clear_moe_layer_status(self.device)  # reported once; later verifies start clean
                 raise ops._lib.HsmoeError(f"moe_layer_kernel: a cross-workgroup wait gave up (status "
                                           f"{max(vals[2:])}); this verify's outputs are not valid")
             n_accept, bonus_row = vals[0], vals[1]

@@ -140,6 +140,26 @@ class HbmExpertStore:
             self._shared_entries[layer] = t
         return t
 
+    # ------------------------------------------------------------ integrity
+    def expert_record(self, layer: int, eid: int) -> torch.Tensor:
+        """uint8 view of one routed expert's record [w1 | w3 | w2 | s1 | s3 | s2]."""
+        base = self._expert_base(layer, eid)
+        return self.buf[base: base + self.expert_bytes]
+
+    def layer_region(self, layer: int) -> torch.Tensor:
+        """uint8 view of one layer's routed experts (n_experts records)."""
+        if not 0 <= layer < self.n_layers:
+            raise IndexError(f"layer {layer} outside the store")
+        base = layer * self.n_experts * self.expert_bytes
+        return self.buf[base: base + self.n_experts * self.expert_bytes]
+
+    def checksum(self, region: torch.Tensor | None = None) -> torch.Tensor:
+        """XOR of the 16-byte words of `region` (a view of this store, e.g.
+        layer_region(l) or expert_record(l, e)), or of the whole store: uint8
+        [16] on the device (hsmoe_xor_checksum), to compare with a checksum of
+        the source bytes after a load."""
+        return ops.xor_checksum(self.buf if region is None else region)
+
     # ------------------------------------------------------------ fill
     def fill_synthetic(self, seed: int, layers=None) -> None:
         """Fills experts (and shared experts) with the seeded synthetic weights."""

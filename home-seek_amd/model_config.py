@@ -16,5 +16,6 @@ class MoEConfig:
     num_experts_per_tok: int = 6         # :28
     routed_scaling_factor: float = 1.5   # :29
     num_hash_layers: int = 3             # :33
+    tie_word_embeddings: bool = False    # :40
     mtp_num_draft: int = 2               # hardware_config.py:64
     cublas_max_tokens: int = 8           # hardware_config.py:43

@@ -14,27 +14,35 @@ from ._lib import SCALE_E8M0, SCALE_F32, check, lib, ptr, require_cuda, stream_p
 
 __all__ = [
     "SCALE_E8M0", "SCALE_F32", "scale_kind_of", "fp4_dequant_bf16", "fp8_dequant_bf16", "router_topk",
-    "moe_decode", "moe_layer_decode", "moe_layer_decode_routed", "moe_layer_status", "moe_layer_status_words", "lm_head_accept", "expert_table",
-    "shared_entry", "MAX_DECODE_TOKENS", "MAX_LAYER_EXPERTS",
+    "moe_decode", "moe_layer_decode", "moe_layer_decode_routed", "moe_layer_status", "moe_layer_status_words",
+    "clear_moe_layer_status", "check_moe_layer_status", "lm_head_accept", "expert_table", "shared_entry",
+    "dequant_blocked", "xor_checksum", "MAX_DECODE_TOKENS", "MAX_LAYER_EXPERTS",
 ]
 
 MAX_DECODE_TOKENS = 8
 MAX_LAYER_EXPERTS = 256  # expert count the one-launch layer kernel handles
 
 _workspaces: dict[tuple, torch.Tensor] = {}
+# Workspaces replaced by larger ones.  A HIP graph captured before the growth
+# still holds the old address, so the old tensor stays allocated for the life
+# of the process (a graph replay must never touch freed memory).
+_retired_workspaces: list[tuple[tuple, torch.Tensor]] = []
 
 
 def _workspace(device: torch.device, purpose: str, nbytes: int) -> torch.Tensor:
     """Zero-filled device workspace of at least nbytes, one per (device,
     stream, purpose), grown when a call needs more.  A grown layer workspace
-    keeps the sticky status word of the one it replaces."""
+    keeps the sticky status word of the one it replaces; the replaced one is
+    kept alive (graphs captured against it may still replay)."""
     key = (device.index, stream_ptr(device), purpose)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         new = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
-        if ws is not None and purpose == "layer":
-            off = lib().hsmoe_moe_layer_status_offset()
-            new[off:off + 4].copy_(ws[off:off + 4])
+        if ws is not None:
+            if purpose == "layer":
+                off = lib().hsmoe_moe_layer_status_offset()
+                new[off:off + 4].copy_(ws[off:off + 4])
+            _retired_workspaces.append((key, ws))
         ws = new
         _workspaces[key] = ws
     return ws
@@ -88,6 +96,35 @@ def fp8_dequant_bf16(data: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     out = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
     check(lib().hsmoe_fp8_dequant_bf16(ptr(data), ptr(scale), n, k, ptr(out), stream_ptr(dev)),
           "hsmoe_fp8_dequant_bf16")
+    return out
+
+
+def dequant_blocked(data: torch.Tensor, scale: torch.Tensor, block: tuple[int, int],
+                    out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """[N, K] fp32 or bf16 from FP4 (int8/uint8 packed [N, K/2]) or e4m3 ([N, K])
+    data with fp32 scales, one per (block[0] x block[1]) block (hsmoe_dequant_blocked)."""
+    dev = require_cuda(data, scale)
+    if data.dim() != 2:
+        raise ValueError("dequant_blocked takes 2-D data")
+    if data.dtype in (torch.int8, torch.uint8):
+        kind, k = _lib.DATA_FP4, data.shape[1] * 2
+    elif data.dtype == torch.float8_e4m3fn:
+        kind, k = _lib.DATA_E4M3, data.shape[1]
+    else:
+        raise TypeError(f"dequant_blocked takes packed FP4 (int8) or float8_e4m3fn data, got {data.dtype}")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("dequant_blocked writes fp32 or bf16")
+    br, bc = int(block[0]), int(block[1])
+    n = data.shape[0]
+    scale = scale.to(torch.float32)
+    if scale.dim() != 2 or br < 1 or bc < 1 or scale.shape[0] * br < n or scale.shape[1] * bc < k:
+        raise ValueError(f"scale {tuple(scale.shape)} with block {tuple(block)} does not cover [{n}, {k}]")
+    scale = scale.contiguous()
+    data = data.contiguous().view(torch.uint8)
+    out = torch.empty(n, k, dtype=out_dtype, device=dev)
+    check(lib().hsmoe_dequant_blocked(ptr(data), kind, ptr(scale), n, k, br, bc, scale.shape[1], ptr(out),
+                                      _lib.OUT_F32 if out_dtype == torch.float32 else _lib.OUT_BF16,
+                                      stream_ptr(dev)), "hsmoe_dequant_blocked")
     return out
 
 
@@ -322,7 +359,9 @@ def moe_layer_decode_routed(x: torch.Tensor, topk_idx: torch.Tensor, table: torc
 
 
 def _layer_workspaces(device: torch.device, stream: int | None = None) -> list[torch.Tensor]:
-    return [ws for (d, st, purpose), ws in _workspaces.items()
+    """The layer workspaces of `stream` (or of every stream) on the device,
+    the retired ones included (a graph captured against one still writes it)."""
+    return [ws for (d, st, purpose), ws in list(_workspaces.items()) + _retired_workspaces
             if purpose == "layer" and d == device.index and (stream is None or st == stream)]
 
 
@@ -347,10 +386,21 @@ def moe_layer_status(device: torch.device | None = None, stream: int | None = No
     return status
 
 
+def clear_moe_layer_status(device: torch.device | None = None, stream: int | None = None) -> None:
+    """Zeroes the sticky status words (of `stream`'s layer workspaces, or of
+    every stream of the device), stream-ordered on the current stream, so that
+    a reported give-up does not fail every later launch's check."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    for w in moe_layer_status_words(device, stream):
+        w.zero_()
+
+
 def check_moe_layer_status(device: torch.device | None = None, stream: int | None = None) -> None:
-    """Raises HsmoeError when moe_layer_status is not 0."""
+    """Raises HsmoeError when moe_layer_status is not 0; the status words are
+    cleared first, so the error is reported once."""
     st = moe_layer_status(device, stream)
     if st:
+        clear_moe_layer_status(device, stream)
         raise _lib.HsmoeError(f"moe_layer_kernel: a cross-workgroup wait gave up (status {st}); "
                               "the outputs of that launch are not valid")
 
@@ -410,6 +460,23 @@ def add_rms_norm(x: torch.Tensor, weight: torch.Tensor, add: torch.Tensor | None
     check(lib().hsmoe_add_rms_norm(ptr(x2), ptr(add), ptr(residual), ptr(w), x2.shape[0], d, eps, ptr(h), ptr(out),
                                    stream_ptr(dev)), "hsmoe_add_rms_norm")
     return (None if h is None else h.reshape(shape)), out.reshape(shape)
+
+
+def xor_checksum(data: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """uint8 [16] device tensor: the XOR of the 16-byte words of `data`'s bytes
+    (a contiguous device tensor whose byte size is a multiple of 16)."""
+    dev = require_cuda(data, out)
+    if not data.is_contiguous():
+        raise ValueError("xor_checksum needs a contiguous tensor")
+    nbytes = data.numel() * data.element_size()
+    if out is None:
+        out = torch.empty(16, dtype=torch.uint8, device=dev)
+    elif out.numel() * out.element_size() != 16 or not out.is_contiguous():
+        raise ValueError("xor_checksum out must be 16 contiguous bytes")
+    ws = _workspace(dev, "checksum", lib().hsmoe_xor_checksum_workspace_size())
+    check(lib().hsmoe_xor_checksum(ptr(data) if nbytes else None, nbytes, ptr(out), ptr(ws), ws.numel(),
+                                   stream_ptr(dev)), "hsmoe_xor_checksum")
+    return out
 
 
 # ---------------------------------------------------------------- generators

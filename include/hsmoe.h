@@ -70,6 +70,27 @@ int hsmoe_fp8_dequant_bf16(const void* data_dev, const float* scale_dev, int64_t
                            hsmoe_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Block-scaled dequant of FP4 or FP8 data with any block shape, to fp32 or bf16.
+ *   out[n, c] = fp32(code[n, c]) * scale[n / block_rows, c / block_cols]   (one fp32 rounding)
+ *   bf16 output: that fp32 value rounded to nearest even.
+ * Replaces cast_back for every block size (reference src/home_seek/_fp4.py:98-110:
+ * repeat_interleave of the scales, product in fp32, then .to(fp32 | bf16)) and,
+ * with one scale 1.0 covering the whole tensor, unpack_from_e2m1fn_x2
+ * (_fp4.py:72-95) for any row length.
+ * data_kind HSMOE_DATA_FP4: packed bytes [n_rows, k/2] (low nibble = even
+ * column, k even); HSMOE_DATA_E4M3: bytes [n_rows, k].  scale: fp32 rows of
+ * scale_cols >= ceil(k / block_cols) entries, ceil(n_rows / block_rows) rows.
+ * out: [n_rows, k] fp32 (HSMOE_OUT_F32) or bf16 (HSMOE_OUT_BF16), contiguous.
+ */
+#define HSMOE_DATA_FP4 0
+#define HSMOE_DATA_E4M3 1
+#define HSMOE_OUT_F32 0
+#define HSMOE_OUT_BF16 1
+int hsmoe_dequant_blocked(const void* data_dev, int data_kind, const float* scale_dev, int64_t n_rows, int64_t k,
+                          int64_t block_rows, int64_t block_cols, int64_t scale_cols, void* out_dev, int out_kind,
+                          hsmoe_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Router: sqrt(softplus) scores, stable top-k, renormalised weights.
  * Replaces compute_expert_affinity_with_bias / compute_expert_affinity
  * (reference src/home_seek/router.py:10-36) as called by
@@ -278,6 +299,21 @@ int hsmoe_rms_norm(const void* x_dev, const void* w_dev, int64_t rows, int64_t d
  * is this entry point with add = res = h_out = NULL. */
 int hsmoe_add_rms_norm(const void* x_dev, const void* add_dev, const void* res_dev, const void* w_dev, int64_t rows,
                        int64_t d, float eps, void* h_out_dev, void* out_dev, hsmoe_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * XOR checksum of a device buffer: out (16 bytes) = XOR of the buffer's
+ * 16-byte words.  Verifies the HBM expert store (or any slice of it) against a
+ * host-side checksum of the same bytes; the checksum of a concatenation is
+ * the XOR of its pieces' checksums.  No counterpart in the reference, whose
+ * weight loader checks shapes only (src/home_seek/inference_engine/
+ * weight_loader.py:48-134); it is also the library's read-only stream, the
+ * measure of the HBM read rate a single pass over the weights can reach.
+ * nbytes % 16 == 0 (0 gives zeros); data and out 16-byte aligned; workspace of
+ * hsmoe_xor_checksum_workspace_size() bytes, any contents.
+ */
+size_t hsmoe_xor_checksum_workspace_size(void);
+int hsmoe_xor_checksum(const void* data_dev, int64_t nbytes, void* out_dev, void* workspace_dev,
+                       size_t workspace_bytes, hsmoe_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Synthetic data generators (counter-based, reproducible on the host): value i

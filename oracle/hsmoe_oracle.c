@@ -20,6 +20,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define HSO_API __attribute__((visibility("default")))
@@ -154,9 +155,11 @@ HSO_API void hso_dequant_fp8_block(const uint8_t* data, const float* scale, int6
  * If bias != NULL, follows router.py:28-29: bf16(bf16(logit) + bf16(bias)). */
 HSO_API void hso_logits_bf16(const uint16_t* x, const uint16_t* w, const float* bias, int64_t m_rows,
                              int64_t n_rows, int64_t k, uint16_t* out) {
-  double xs[8192];
+  /* one token's hidden row widened to fp64, for any k */
+  double* xs = (double*)malloc((size_t)(k > 0 ? k : 1) * sizeof(double));
+  if (!xs) abort();
   for (int64_t m = 0; m < m_rows; ++m) {
-    for (int64_t c = 0; c < k && c < 8192; ++c) xs[c] = (double)hso_bf16_to_f32(x[m * k + c]);
+    for (int64_t c = 0; c < k; ++c) xs[c] = (double)hso_bf16_to_f32(x[m * k + c]);
     for (int64_t r = 0; r < n_rows; ++r) {
       const uint16_t* wr = w + r * k;
       double acc = 0.0;
@@ -169,6 +172,7 @@ HSO_API void hso_logits_bf16(const uint16_t* x, const uint16_t* w, const float* 
       out[m * n_rows + r] = l;
     }
   }
+  free(xs);
 }
 
 /* ------------------------------------------------------------------ */

@@ -143,6 +143,38 @@ def dequant_fp8(data: np.ndarray, scale: np.ndarray) -> np.ndarray:
     return out
 
 
+def cast_back(data: np.ndarray, fp4: bool, scale: np.ndarray, block: tuple[int, int], out_f32: bool) -> np.ndarray:
+    """_fp4.py:98-110 for any block: the decoded values (unpack_from_e2m1fn_x2,
+    _fp4.py:72-95, or e4m3 -> fp32) times the scale of each element's
+    (block[0] x block[1]) block -- the scales repeat_interleave'd along both
+    axes and cut to the data's shape -- as one fp32 multiply; returned as fp32,
+    or as bf16 bits (RNE).  data: packed FP4 bytes [N, K/2] or e4m3 bytes [N, K]."""
+    data = np.ascontiguousarray(data).view(np.uint8)
+    if fp4:
+        codes = np.empty((data.shape[0], data.shape[1] * 2), dtype=np.uint8)
+        codes[:, 0::2] = data & 0x0F
+        codes[:, 1::2] = data >> 4
+        vals = e2m1_table()[codes]
+    else:
+        vals = e4m3_table()[data]
+    n, k = vals.shape
+    sf = np.asarray(scale, dtype=np.float32)
+    sf = np.repeat(np.repeat(sf, block[0], axis=0), block[1], axis=1)[:n, :k]
+    prod = (vals.astype(np.float32) * sf).astype(np.float32)
+    return prod if out_f32 else f32_to_bf16(prod)
+
+
+def xor_checksum(buf: np.ndarray) -> np.ndarray:
+    """uint8 [16]: the XOR of the buffer's 16-byte words (hsmoe_xor_checksum;
+    no reference counterpart: the store-integrity check of this build)."""
+    b = np.ascontiguousarray(buf).view(np.uint8).reshape(-1)
+    if b.size % 16:
+        raise ValueError("xor_checksum takes a multiple of 16 bytes")
+    if b.size == 0:
+        return np.zeros(16, dtype=np.uint8)
+    return np.bitwise_xor.reduce(b.view(np.uint64).reshape(-1, 2), axis=0).view(np.uint8)
+
+
 # ------------------------------------------------------------------ RNG (workload generator)
 
 KIND_FP4_DATA, KIND_FP4_SCALE, KIND_GATE_W, KIND_GATE_BIAS, KIND_HIDDEN = 1, 2, 3, 4, 5

@@ -104,7 +104,9 @@ def test_router_ties_and_no_bias(dev):
      # 4-row tiles than waves
      (3, 3001, 512), (4, 20001, 1536), (2, 5, 1536),
      # six tokens of 4096: fp64 hidden states past the LDS budget, widened into the workspace by a launch of their own
-     (6, 3001, 4096)])
+     (6, 3001, 4096),
+     # the largest hidden size the entry point takes: 64 KiB of bf16 hidden states in the MFMA form's LDS
+     (2, 3001, 8192), (3, 1001, 8192), (4, 2049, 8192), (1, 1001, 8192)])
 def test_lm_head_logits_argmax_bit_exact(dev, n_tok, vocab, d):
     seed = 7 + n_tok
     lm = synthetic.normal_bf16(seed, synthetic.tag(synthetic.KIND_LM_HEAD), (vocab, d), 0.0, 0.02, dev)

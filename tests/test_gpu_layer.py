@@ -198,7 +198,7 @@ def test_workspace_rearms_before_the_tags_wrap(layer, dev):
     x = synthetic.hidden(SEED, 700, 3, D, dev)
     ref = staged(x, gate, bias, store.table(0), store.shared_entry(0))
     fused(x, gate, bias, store.table(0), store.shared_entry(0))
-    (ws,) = ops._layer_workspaces(dev, ops.stream_ptr(dev))
+    ws = ops._workspaces[(dev.index, ops.stream_ptr(dev), "layer")]  # the current one (not the retired)
     epoch = ws[0:4].view(torch.int32)
     epoch.fill_(0x7FFFFFFE)
     ctl = 4096

@@ -234,6 +234,38 @@ def test_verify_reads_status_and_accepts(model):
         assert so.argmax(np16(bonus)) == so.argmax(lv[row:row + 1])
 
 
+def test_status_word_raises_once_and_restores_position(model):
+    """A nonzero sticky status word (written from the host: no kernel gives up
+    here) makes _mtp_verify_batched and GreedyDecoder.result() raise
+    HsmoeError, restores _global_pos, and is cleared by the report, so the
+    next verify runs clean."""
+    from home_seek_amd._lib import HsmoeError
+    from home_seek_amd.engine import GreedyDecoder
+    eng, so = model
+    dev = eng.device
+    a = so.next_token(55)
+    drafts = torch.tensor([[so.next_token(a), 3]], dtype=torch.int64, device=dev)
+    main = torch.tensor([[a]], dtype=torch.int64, device=dev)
+    assert eng._mtp_verify_batched(drafts, 0.0, main_pred_id=main)[0] == 1  # creates the layer workspaces
+    words = ops.moe_layer_status_words(dev)
+    assert words and all(int(w.item()) == 0 for w in words)
+    pos = eng._global_pos
+    words[0].fill_(1 + 4609)
+    with pytest.raises(HsmoeError):
+        eng._mtp_verify_batched(drafts, 0.0, main_pred_id=main)
+    assert eng._global_pos == pos
+    assert ops.moe_layer_status(dev) == 0
+    assert eng._mtp_verify_batched(drafts, 0.0, main_pred_id=main)[0] == 1
+    dec = GreedyDecoder(eng, 2, graph=False)
+    dec.reset(9)
+    dec.run(1)
+    ops.moe_layer_status_words(dev)[-1].fill_(1 + 4611)
+    with pytest.raises(HsmoeError):
+        dec.result()
+    assert ops.moe_layer_status(dev) == 0
+    assert dec.result()[0][0] == so.next_token(9)
+
+
 def test_loader_entries_match_oracle(model):
     """The reference-shaped loaders: _load_expert_weights gives int8 data and
     fp32 scales equal to the E8M0 values 2^(e-127); _load_bf16_deq and
