@@ -59,9 +59,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="default 800 (headline) / 64 (stack) / 50 (prefill)")
     ap.add_argument("--warmup", type=int, default=None, help="default 40 (headline) / 4 (stack) / 5 (prefill)")
-    ap.add_argument("--workload", choices=("all", "layer", "verify", "stack", "prefill"), default="all",
+    ap.add_argument("--workload", choices=("all", "layer", "expert", "verify", "stack", "prefill"), default="all",
                     help="all: the headline layer line with configs 0, 2, 3, 4 under 'configs'; "
-                         "layer: the headline only; verify / stack / prefill: config 2 / 4 / 3 as the line")
+                         "layer: the headline only; expert / verify / stack / prefill: config 0 / 2 / 4 / 3 as "
+                         "the line")
     ap.add_argument("--configs", default="0,2,3,4", help="sub-workloads of --workload all")
     ap.add_argument("--stack-layers", type=int, default=43)
     ap.add_argument("--stack-steps", type=int, default=16, help="decode steps of config 4 under --workload all")
@@ -132,6 +133,38 @@ def roofline(kernel: str, nbytes: int, us: float, traffic=None, **extra) -> dict
     return {"bound": "hbm", "kernel": kernel, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "algorithmic_bytes_per_launch": nbytes,
             "avg_launch_us": round(us, 3), **extra}
+
+
+def read_ceiling(torch, buf, stream) -> dict:
+    """The HBM read rate a single pass over resident weights reaches on this
+    device: hsmoe_xor_checksum (a read-only stream, 16 loads of 16 bytes in
+    flight per lane) over distinct 1 GiB slices of `buf` in rotation, far
+    beyond the 256 MB Infinity Cache; median of the per-replay rates."""
+    from home_seek_amd import ops
+    gib = 1 << 30
+    n = min(8, buf.numel() // gib)
+    if n < 2:
+        return None
+    slices = [buf[j * gib:(j + 1) * gib] for j in range(n)]
+    outs = [torch.empty(16, dtype=torch.uint8, device=buf.device) for _ in range(n)]
+    _, samples = timed_launches(torch, stream, lambda j: ops.xor_checksum(slices[j], outs[j]), n, 4 * n, n)
+    us = statistics.median(samples)
+    return {"gbs": round(gib / (us * 1e-6) / 1e9, 1), "bytes_per_launch": gib, "us_per_launch": round(us, 2),
+            "slices": n, "frac_of_hbm_peak": round(gib / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "method": "hsmoe_xor_checksum over distinct 1 GiB slices of the expert store, rotated in a HIP graph "
+                      "(the stream launch + a one-workgroup fold); median of per-replay times"}
+
+
+def with_ceiling(roof: dict | None, ceiling: dict | None) -> dict | None:
+    """Adds the fraction of the measured read ceiling to a roofline (and its nested ones)."""
+    if roof is None or not ceiling:
+        return roof
+    roof["read_ceiling_gbs"] = ceiling["gbs"]
+    roof["frac_of_read_ceiling"] = round(roof["achieved"] / ceiling["gbs"], 4)
+    for v in roof.values():
+        if isinstance(v, dict) and "achieved" in v:
+            with_ceiling(v, ceiling)
+    return roof
 
 
 def pmc_traffic(name: str):
@@ -354,7 +387,8 @@ def run_config0(torch, args, lb: LayerBench, cpu_info):
     us = sp["median_us"]
     gbs = EXPERT_BYTES / (us * 1e-6) / 1e9
     res = {"workload": "config 0: one routed FP4 expert (dequant + SwiGLU FFN), M=1, D=4096 I=2048",
-           "value": round(gbs, 1), "unit": "GB/s", "steps": steps, "ms_per_step": round(us * 1e-3, 5),
+           "value": round(gbs, 1), "unit": "GB/s", "steps": steps, "warmup": len(pairs),
+           "ms_per_step": round(us * 1e-3, 5),
            "timing": sp, "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
            "roofline": roofline("moe_layer_kernel with one given id (one launch)", EXPERT_BYTES + 2 * D * 2, us),
            "cpu_baseline": None}
@@ -462,7 +496,7 @@ def run_config2(torch, args, lb: LayerBench, cpu_info):
 
 # ---------------------------------------------------------------- config 3
 
-def run_prefill(torch, args, cpu_info, steps=None, warmup=None):
+def run_prefill(torch, args, cpu_info, steps=None, warmup=None, ceiling=None):
     """Prefill MoE layer: M=512 tokens, 256 FP4 experts, top-6 with Zipf(1.1)
     popularity drawn without replacement per token, routed experts only (the
     shared expert timed separately); one hsmoe_moe_prefill call (group,
@@ -507,6 +541,10 @@ def run_prefill(torch, args, cpu_info, steps=None, warmup=None):
            "roofline": roofline("hsmoe_moe_prefill call (group + gate/up + down + combine launches)",
                                 routed_bytes + io_bytes, us, pmc_traffic("prefill_m512_pmc.json")),
            "cpu_baseline": None}
+    if ceiling is None:
+        ceiling = read_ceiling(torch, store.buf, stream)
+        res["read_ceiling"] = ceiling
+    with_ceiling(res["roofline"], ceiling)
     if not args.no_cpu_baseline:
         from oracle import cpu_ref
         union = [e for e in range(E) if counts[e]][:8]
@@ -529,7 +567,7 @@ def run_prefill(torch, args, cpu_info, steps=None, warmup=None):
 
 # ---------------------------------------------------------------- config 4
 
-def run_stack(torch, args, cpu_info, steps=None, warmup=None):
+def run_stack(torch, args, cpu_info, steps=None, warmup=None, ceiling=None):
     """The MoE-only decode stack: all layers' experts resident, greedy decode with
     MTP verify, one step = M=1 forward + 2 MTP drafts + T=3 verify, captured as
     one HIP graph and replayed; tok/s over the timed steps."""
@@ -614,6 +652,10 @@ def run_stack(torch, args, cpu_info, steps=None, warmup=None):
            "roofline": roofline("whole decode step (all kernels of one graph replay)", total // steps, ms / steps * 1e3,
                                 lm_head_bytes_per_step=lm_bytes // steps),
            "build_s": round(t_build, 1), "wall_s_timed": round(wall, 3), "cpu_baseline": None}
+    if ceiling is None:
+        ceiling = read_ceiling(torch, eng.store.buf, torch.cuda.Stream())
+        res["read_ceiling"] = ceiling
+    with_ceiling(res["roofline"], ceiling)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = stack_cpu_baseline(torch, eng, rows[0], n_layers, res["tokens_per_step"], args, cpu_info)
     del eng, dec
@@ -697,10 +739,13 @@ def main():
     __graft_entry__.package()
     torch.cuda.set_device(0)
     cpu_info = cpu_setup() if not args.no_cpu_baseline else {"threads": 0}
-    if args.workload in ("verify", "stack", "prefill"):
-        if args.workload == "verify":
-            res = run_config2(torch, args, LayerBench(torch, args), cpu_info)
-            res["warmup"] = args.layers
+    if args.workload in ("verify", "stack", "prefill", "expert"):
+        if args.workload in ("verify", "expert"):
+            lb = LayerBench(torch, args)
+            res = (run_config2 if args.workload == "verify" else run_config0)(torch, args, lb, cpu_info)
+            res.setdefault("warmup", args.layers)
+            res["read_ceiling"] = read_ceiling(torch, lb.store.buf, lb.stream)
+            with_ceiling(res["roofline"], res["read_ceiling"])
         else:
             fn = run_stack if args.workload == "stack" else run_prefill
             res = fn(torch, args, cpu_info)
@@ -719,6 +764,9 @@ def main():
 
     lb = LayerBench(torch, args)
     line = run_headline(torch, args, lb, cpu_info)
+    ceiling = read_ceiling(torch, lb.store.buf, lb.stream)
+    line["read_ceiling"] = ceiling
+    with_ceiling(line["roofline"], ceiling)
     if args.workload == "all":
         want = [c.strip() for c in args.configs.split(",") if c.strip()]
         configs = {}
@@ -738,6 +786,8 @@ def main():
         if "4" in want:
             print("[bench] config 4", file=sys.stderr, flush=True)
             configs["4"] = run_stack(torch, args, cpu_info, steps=args.stack_steps, warmup=2)
+        for res in configs.values():
+            with_ceiling(res.get("roofline"), ceiling)
         line["configs"] = configs
     calib_copy(torch, args)
     print(json.dumps(line))

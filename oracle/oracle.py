@@ -316,11 +316,15 @@ def _swiglu_f32(g: np.ndarray, u: np.ndarray, limit: float) -> np.ndarray:
 
 def expert_ffn_fp32(x: np.ndarray, w1: np.ndarray, w3: np.ndarray, w2: np.ndarray, limit: float = 10.0) -> np.ndarray:
     """fused_expert_ffn_pt (fused_moe.py:383-395) with fp32 accumulation and fp32 intermediates -> fp32 [M, D]."""
-    xf = bf16_to_f32(x)
-    gate = xf @ bf16_to_f32(w1).T
-    up = xf @ bf16_to_f32(w3).T
+    return _ffn_f32w(bf16_to_f32(x), bf16_to_f32(w1), bf16_to_f32(w3), bf16_to_f32(w2), limit)
+
+
+def _ffn_f32w(xf: np.ndarray, w1f: np.ndarray, w3f: np.ndarray, w2f: np.ndarray, limit: float) -> np.ndarray:
+    """expert_ffn_fp32 on fp32 copies of x and the weights (the same operations)."""
+    gate = xf @ w1f.T
+    up = xf @ w3f.T
     act = _swiglu_f32(gate.astype(np.float32), up.astype(np.float32), limit)
-    return (act @ bf16_to_f32(w2).T).astype(np.float32)
+    return (act @ w2f.T).astype(np.float32)
 
 
 def expert_ffn_ref_bf16(x: np.ndarray, w1: np.ndarray, w3: np.ndarray, w2: np.ndarray,
@@ -357,6 +361,59 @@ def moe_layer_fp32(x: np.ndarray, idx: np.ndarray, w: np.ndarray, experts: dict,
     if shared is not None:
         out = (out + expert_ffn_fp32(x, shared["w1_bf16"], shared["w3_bf16"], shared["w2_bf16"], limit)).astype(
             np.float32)
+    return out
+
+
+def moe_layer_fp32_lazy(x: np.ndarray, idx: np.ndarray, w: np.ndarray, expert_fn, shared_fn, limit: float = 10.0,
+                        pool=None) -> np.ndarray:
+    """moe_layer_fp32 with experts produced on demand by expert_fn(e) (a dict as
+    gen_fp4_expert, or None when absent) and the shared one by shared_fn() (or
+    None), never held all at once: each distinct expert is generated, its
+    weights widened to fp32 once, and its FFN evaluated for every (token, slot)
+    that selects it -- each token row alone, with the same operations as
+    moe_layer_fp32 -- on `pool` (a concurrent.futures executor) when given.
+    The terms are then added in moe_layer_fp32's order, so the result is the
+    same bit for bit."""
+    m, d = x.shape
+    xf = bf16_to_f32(x)
+    uses: dict[int, list[int]] = {}
+    for t in range(m):
+        for j in range(idx.shape[1]):
+            e = int(idx[t, j])
+            if e >= 0:
+                uses.setdefault(e, [])
+                if t not in uses[e]:
+                    uses[e].append(t)
+
+    def one(e):
+        ex = expert_fn(e)
+        if ex is None:
+            return e, None
+        w1f, w3f, w2f = (bf16_to_f32(ex[k]) for k in ("w1_bf16", "w3_bf16", "w2_bf16"))
+        return e, {t: _ffn_f32w(xf[t:t + 1], w1f, w3f, w2f, limit)[0] for t in uses[e]}
+
+    def shared_one():
+        sh = shared_fn() if shared_fn is not None else None
+        if sh is None:
+            return None
+        return _ffn_f32w(xf, *(bf16_to_f32(sh[k]) for k in ("w1_bf16", "w3_bf16", "w2_bf16")), limit)
+
+    if pool is None:
+        ys = dict(one(e) for e in uses)
+        ysh = shared_one()
+    else:
+        fsh = pool.submit(shared_one)
+        ys = dict(pool.map(one, list(uses)))
+        ysh = fsh.result()
+    out = np.zeros((m, d), dtype=np.float32)
+    for t in range(m):
+        for j in range(idx.shape[1]):
+            e = int(idx[t, j])
+            if e < 0 or ys.get(e) is None:
+                continue
+            out[t] = (out[t] + np.float32(w[t, j]) * ys[e][t]).astype(np.float32)
+    if ysh is not None:
+        out = (out + ysh).astype(np.float32)
     return out
 
 

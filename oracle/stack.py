@@ -42,10 +42,21 @@ class StackOracle:
     """The synthetic stack of seed `seed` at any size (store layer n_layers = MTP block)."""
 
     def __init__(self, seed: int, n_layers: int, n_experts: int, d: int, i: int, vocab: int, top_k: int = 6,
-                 n_hash: int = 3, scaling: float = 1.5, limit: float = 10.0, eps: float = 1e-6):
+                 n_hash: int = 3, scaling: float = 1.5, limit: float = 10.0, eps: float = 1e-6,
+                 cache: bool = True, workers: int = 0):
+        """cache=False regenerates experts on every use (host memory stays at
+        the few experts in flight: a full-size stack holds 11,008 of them);
+        workers > 0 evaluates a layer's experts and logits rows on that many
+        threads (the C generators and numpy release the GIL), with results
+        equal to the serial ones bit for bit."""
         self.seed, self.n_layers, self.E, self.d, self.i = seed, n_layers, n_experts, d, i
         self.vocab, self.k, self.n_hash = vocab, top_k, n_hash
         self.scaling, self.limit, self.eps = scaling, limit, eps
+        self.cache = cache
+        self._pool = None
+        if workers > 0:
+            from concurrent.futures import ThreadPoolExecutor
+            self._pool = ThreadPoolExecutor(max_workers=workers)
         self._experts: dict = {}
         self._shared: dict = {}
         self.layers = [self._layer_weights(l, hashed=l < n_hash) for l in range(n_layers)]
@@ -77,11 +88,15 @@ class StackOracle:
         return lw
 
     def expert(self, layer: int, eid: int) -> dict:
+        if not self.cache:
+            return orc.gen_fp4_expert(self.seed, layer, eid, self.d, self.i)
         if (layer, eid) not in self._experts:
             self._experts[(layer, eid)] = orc.gen_fp4_expert(self.seed, layer, eid, self.d, self.i)
         return self._experts[(layer, eid)]
 
     def shared(self, layer: int) -> dict:
+        if not self.cache:
+            return orc.gen_shared_expert(self.seed, layer, self.d, self.i)
         if layer not in self._shared:
             self._shared[layer] = orc.gen_shared_expert(self.seed, layer, self.d, self.i)
         return self._shared[layer]
@@ -97,8 +112,11 @@ class StackOracle:
     def ffn(self, hn: np.ndarray, lw: dict, layer: int, ids) -> tuple[np.ndarray, np.ndarray]:
         """Routed + shared FFN of normed hidden hn [T, D] -> (fp32 out [T, D], idx)."""
         idx, w = self.route(hn, lw, ids)
-        experts = {int(e): self.expert(layer, int(e)) for e in np.unique(idx)}
-        return orc.moe_layer_fp32(hn, idx, w, experts, self.shared(layer), self.limit), idx
+        if self.cache and self._pool is None:
+            experts = {int(e): self.expert(layer, int(e)) for e in np.unique(idx)}
+            return orc.moe_layer_fp32(hn, idx, w, experts, self.shared(layer), self.limit), idx
+        return orc.moe_layer_fp32_lazy(hn, idx, w, lambda e: self.expert(layer, e), lambda: self.shared(layer),
+                                       self.limit, self._pool), idx
 
     def layer(self, h: np.ndarray, lw: dict, layer: int, ids) -> dict:
         """One layer on bf16 h [T, D] -> {"h1": h + r, "hn": normed, "ffn": fp32, "idx", "out": bf16}."""
@@ -118,19 +136,26 @@ class StackOracle:
         return h
 
     def logits(self, h: np.ndarray, norm_w: np.ndarray) -> np.ndarray:
-        return orc.logits_bf16(orc.rms_norm(h, norm_w, self.eps), self.lm_head)
+        hn = orc.rms_norm(h, norm_w, self.eps)
+        if self._pool is None or hn.shape[0] == 1:
+            return orc.logits_bf16(hn, self.lm_head)
+        rows = list(self._pool.map(lambda t: orc.logits_bf16(hn[t:t + 1], self.lm_head), range(hn.shape[0])))
+        return np.concatenate(rows, axis=0)
 
     def argmax(self, logits: np.ndarray) -> list[int]:
         return [orc.argmax_first(logits[t]) for t in range(logits.shape[0])]
 
-    def drafts(self, h_last: np.ndarray, tok: int, n: int = 2) -> list[int]:
+    def drafts(self, h_last: np.ndarray, tok: int, n: int = 2, margins: list | None = None) -> list[int]:
         mw = self.mtp
         h_prev, out = h_last.reshape(1, self.d), []
         for _ in range(n):
             e = orc.rms_norm(self.embed([tok]), mw["enorm"], self.eps)
             h_in = bf16_add(orc.rms_norm(h_prev, mw["hnorm"], self.eps), e)
             h_prev = self.layer(h_in, mw["layer"], mw["layer_idx"], [tok])["out"]
-            tok = self.argmax(self.logits(h_prev, mw["norm"]))[0]
+            lg = self.logits(h_prev, mw["norm"])
+            if margins is not None:
+                margins.append(top2_gap(lg[0]))
+            tok = self.argmax(lg)[0]
             out.append(tok)
         return out
 
@@ -149,7 +174,7 @@ class StackOracle:
             margins.append(top2_gap(lg[0]))
         if n_draft == 0 and draft_fn is None:
             return [a], 1, a, 0
-        dr = self.drafts(h, a, n_draft) if draft_fn is None else list(draft_fn(h, a))
+        dr = self.drafts(h, a, n_draft, margins) if draft_fn is None else list(draft_fn(h, a))
         combined = [a] + dr
         lv = self.logits(self.forward_stack(combined), self.final_norm)
         if margins is not None:

@@ -24,7 +24,7 @@ import torch
 
 from home_seek_amd import ops, stack
 from oracle import oracle as orc
-from oracle.stack import StackOracle
+from oracle.stack import StackOracle, bf16_add
 
 pytestmark = pytest.mark.gpu
 
@@ -180,3 +180,87 @@ def test_mtp_verify_batched_at_full_vocab(eng):
         want_tok = (d0, d1, device_next(eng, d1))[row]
         assert int(pred[row].item()) == want_tok
     assert ops.moe_layer_status(dev) == 0
+
+
+def test_full_size_decode_step_teacher_forced(eng):
+    """Every kernel call of one full-size decode step (the 43-layer M=1
+    forward, the MTP block's two drafts, the T=3 verify of [A, d0, d1] and the
+    four lm_head passes), checked against the oracle on the inputs the device
+    gave it: each fused residual add + RMSNorm (sum bit-exact, norm within one
+    bf16 step), each layer's FFN (expert ids bit-exact, output within one bf16
+    step plus the 2e-2 bar), each lm_head pass (logits' argmax, accepted count
+    and bonus row bit-exact), and the step's row built from those decisions.
+    The synthetic stack cannot be compared free-running: its residual stream
+    grows to ~1e5 and each layer's bf16 roundings of sums that agree to ~2e-6
+    flip a few elements by a whole bf16 step, which the next layers amplify
+    (relative difference 1e-4 after one layer, 1e-2 after seven, where the
+    first top-6 changes); teacher forcing checks every computation of the
+    step instead.  The oracle regenerates each expert on use (16 threads)."""
+    import time
+    from home_seek_amd.engine import GreedyDecoder
+    calls = []
+    inner_ffn, inner_norm, inner_head = eng._forward_ffn, ops.add_rms_norm, ops.lm_head_accept
+
+    def ffn(hn, lw, layer_idx, input_ids=None, out_f32=None):
+        out, used = inner_ffn(hn, lw, layer_idx, input_ids, out_f32)
+        calls.append(("ffn", np16(hn), lw, layer_idx, None if input_ids is None else input_ids.reshape(-1).tolist(),
+                      np16(out), eng._last_routed_idx.reshape(-1, K).cpu().numpy()))
+        return out, used
+
+    def norm(x, weight, add=None, residual=None, eps=1e-6, want_sum=False):
+        h, hn = inner_norm(x, weight, add=add, residual=residual, eps=eps, want_sum=True)
+        calls.append(("norm", np16(x), None if add is None else np16(add),
+                      None if residual is None else np16(residual.reshape(1, -1))[0], np16(weight.reshape(1, -1))[0],
+                      np16(h), np16(hn)))
+        return (h if want_sum else None), hn
+
+    def head(h, lm_head, ids=None, want_logits=True):
+        lg, pred, res = inner_head(h, lm_head, ids, want_logits)
+        calls.append(("head", np16(h), None if ids is None else ids.reshape(-1).tolist(), pred.cpu().tolist(),
+                      res.cpu().tolist()))
+        return lg, pred, res
+
+    eng._forward_ffn, ops.add_rms_norm, ops.lm_head_accept = ffn, norm, head
+    try:
+        dec = GreedyDecoder(eng, 1, graph=False)
+        dec.reset(31337)
+        dec.run(1)
+    finally:
+        del eng._forward_ffn
+        ops.add_rms_norm, ops.lm_head_accept = inner_norm, inner_head
+    row = dec.rows[0].cpu().tolist()
+    assert ops.moe_layer_status(eng.device) == 0
+    t0 = time.time()
+    so = StackOracle(SEED, NL, E, D, I, V, K, cache=False, workers=16)
+    kinds = [c[0] for c in calls]
+    assert kinds.count("ffn") == 2 * NL + 2 and kinds.count("head") == 4, kinds
+    heads, worst = [], 0.0
+    for c in calls:
+        if c[0] == "norm":
+            _, x, add, res, w, h, hn = c
+            ref = x if add is None else bf16_add(x, add)
+            ref = ref if res is None else bf16_add(ref, res[None, :])
+            assert np.array_equal(h, ref)
+            assert within_one_step(hn, orc.rms_norm(h, w))
+        elif c[0] == "ffn":
+            _, hn, lw, layer, ids, out, idx = c
+            lwo = so.mtp["layer"] if layer == NL else so.layers[layer]
+            f_ref, idx_ref = so.ffn(hn, lwo, layer, ids)
+            assert np.array_equal(idx, idx_ref), layer
+            g, r = orc.bf16_to_f32(out), orc.bf16_to_f32(orc.f32_to_bf16(f_ref))
+            worst = max(worst, float(np.max(np.abs(g - r))))
+            assert not np.any(np.abs(g - r) > np.abs(r) * 2.0 ** -7 + 2e-2), layer
+        else:
+            _, h, ids, pred, res = c
+            lg = orc.logits_bf16(h, so.lm_head)
+            assert pred == so.argmax(lg)
+            if ids is not None and len(ids) > 1:
+                assert res == list(orc.mtp_accept(lg, ids))
+            heads.append((pred, res))
+    # the row from the checked decisions: A, the drafts, the verify's bonus
+    a, d0, d1 = heads[0][0][0], heads[1][0][0], heads[2][0][0]
+    v_pred, (n_acc, bonus_row) = heads[3]
+    assert row == [a, d0, d1, v_pred[bonus_row]]
+    assert int(dec.n_accs[0].item()) == n_acc
+    print(f"row {row}, accepted {n_acc}; {len(calls)} calls checked (FFN max-abs vs bf16(oracle) {worst:.3g}); "
+          f"oracle {time.time() - t0:.0f} s")

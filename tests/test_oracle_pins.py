@@ -254,7 +254,7 @@ class ToyStack(StackOracle):
         out[np.arange(len(h)), [self.f(int(t)) for t in h]] = 1.0
         return orc.f32_to_bf16(out)
 
-    def drafts(self, h_last, tok, n=2):
+    def drafts(self, h_last, tok, n=2, margins=None):
         return self.draft(tok, n)
 
 
