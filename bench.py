@@ -70,6 +70,9 @@ def parse():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU time budget per config")
+    ap.add_argument("--no-chain-check", action="store_true",
+                    help="config 4: skip the greedy-chain check and the expert-byte count after timing (profiling "
+                         "runs: then every decode-step kernel after the build belongs to the warm-up or timed steps)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="finish with 3 copies of a 256 MiB buffer (known bytes) to scale PMC byte counters")
     ap.add_argument("--path", choices=("fused", "staged"), default="fused",
@@ -390,7 +393,8 @@ def run_config0(torch, args, lb: LayerBench, cpu_info):
            "value": round(gbs, 1), "unit": "GB/s", "steps": steps, "warmup": len(pairs),
            "ms_per_step": round(us * 1e-3, 5),
            "timing": sp, "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-           "roofline": roofline("moe_layer_kernel with one given id (one launch)", EXPERT_BYTES + 2 * D * 2, us),
+           "roofline": roofline("moe_layer_kernel with one given id (one launch)", EXPERT_BYTES + 2 * D * 2, us,
+                                pmc_traffic("expert_m1_pmc.json")),
            "cpu_baseline": None}
     if not args.no_cpu_baseline:
         from oracle import cpu_ref
@@ -607,6 +611,12 @@ def run_stack(torch, args, cpu_info, steps=None, warmup=None, ceiling=None):
     rows = dec.rows[:steps].cpu().tolist()
     print(f"[stack] {steps} steps in {ms:.1f} ms, {len(tokens)} tokens", file=sys.stderr, flush=True)
 
+    if args.no_chain_check:
+        sp = spread(samples)
+        return {"workload": f"config 4: {n_layers}-layer MoE-only decode stack (no chain check: profiling run)",
+                "value": round(len(tokens) / (ms * 1e-3), 2), "unit": "tok/s", "steps": steps, "warmup": warmup,
+                "ms_per_step": round(ms / steps, 4), "timing": sp, "tokens": len(tokens),
+                "decode_steps_run": steps + warmup + 1, "build_s": round(t_build, 1), "cpu_baseline": None}
     # Every token's routing is a function of the token alone (no attention), so
     # the M=1 forward of each token gives the experts the verify reads.
     routing = {}
@@ -630,16 +640,27 @@ def run_stack(torch, args, cpu_info, steps=None, warmup=None, ceiling=None):
     for _ in range(len(tokens)):
         t = next_of(t)
         chain.append(t)
-    expert_bytes = 0
-    for r in rows:  # M=1 forward: K distinct experts per layer; verify [A, d0, d1]: their union
+    verify_experts = 0
+    for r in rows:  # verify [A, d0, d1]: the union of the three tokens' experts per layer
         ver = [route_of(x)[0] for x in r[:3]]
         for l in range(n_layers):
-            expert_bytes += (K + len(ver[0][l] | ver[1][l] | ver[2][l])) * EXPERT_BYTES
-    expert_bytes += steps * 2 * K * EXPERT_BYTES                       # MTP block, two drafts
-    shared_bytes = steps * (2 * n_layers + 2) * SHARED_BYTES
-    router_bytes = steps * (2 * (n_layers - 3) + 2) * ROUTER_BYTES
+            verify_experts += len(ver[0][l] | ver[1][l] | ver[2][l])
+    # layer launches at M=1 (main forward + two MTP drafts) and at M=3 (verify), lm_head passes
+    m1_bytes = steps * ((n_layers + 2) * (K * EXPERT_BYTES + SHARED_BYTES) + (n_layers - 3 + 2) * ROUTER_BYTES)
+    m3_bytes = verify_experts * EXPERT_BYTES + steps * (n_layers * SHARED_BYTES + (n_layers - 3) * ROUTER_BYTES)
     lm_bytes = steps * 4 * LM_HEAD_BYTES                                 # main, 2 drafts, verify
-    total = expert_bytes + shared_bytes + router_bytes + lm_bytes
+    total = m1_bytes + m3_bytes + lm_bytes
+    # HBM traffic per step from the kernels' measured traffic / algorithmic ratios (rocprofv3 FETCH_SIZE +
+    # WRITE_SIZE of the same kernels: the M=1 and M=3 layer launches, the lm_head)
+    ratio = {}
+    for key, name in (("m1", "moe_layer_kernel_m1_pmc.json"), ("m3", "moe_layer_kernel_m3_pmc.json"),
+                      ("lm", "lm_head_t3_pmc.json")):
+        pth = ROOT / "profiles" / name
+        if pth.exists():
+            d = json.loads(pth.read_text())
+            ratio[key] = d["traffic_bytes_per_launch"] / d["algorithmic_bytes_per_launch"]
+    traffic = (int((m1_bytes * ratio["m1"] + m3_bytes * ratio["m3"] + lm_bytes * ratio["lm"]) / steps)
+               if len(ratio) == 3 else None)
     sp = spread(samples)
     res = {"workload": f"config 4: {n_layers}-layer MoE-only decode stack (attention replaced by a seeded residual), "
                        f"{E} FP4 experts + FP8 shared per layer, D={D} I={I}, vocab {VOCAB}; per step M=1 forward + "
@@ -650,7 +671,11 @@ def run_stack(torch, args, cpu_info, steps=None, warmup=None, ceiling=None):
            "tokens_per_step": round(len(tokens) / steps, 4), "greedy_chain_match": tokens == chain,
            "layer_status": 0,
            "roofline": roofline("whole decode step (all kernels of one graph replay)", total // steps, ms / steps * 1e3,
-                                lm_head_bytes_per_step=lm_bytes // steps),
+                                traffic, lm_head_bytes_per_step=lm_bytes // steps,
+                                traffic_method="per kernel class: algorithmic bytes x the traffic / algorithmic "
+                                               "ratio rocprofv3 measured for that kernel (profiles/"
+                                               "moe_layer_kernel_m1_pmc.json, moe_layer_kernel_m3_pmc.json, "
+                                               "lm_head_t3_pmc.json)"),
            "build_s": round(t_build, 1), "wall_s_timed": round(wall, 3), "cpu_baseline": None}
     if ceiling is None:
         ceiling = read_ceiling(torch, eng.store.buf, torch.cuda.Stream())

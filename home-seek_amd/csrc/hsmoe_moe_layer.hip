@@ -798,12 +798,25 @@ __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg
   // of token t are combined through the lane that owns column t.
   uint64_t* part = p.part + (int64_t)s * m * p.d;
   if (kShared && wave >= 2) return state;
+  // one routed slot and no shared expert: this item is its row group's only
+  // contributor and writes the rows itself (the value the row-group sum
+  // would give: 0 + the partial), with no round trip through the partials
+  const bool alone = !kShared && sh.n_routed == 1 && !p.shared;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int col = lane & 15;
     const float lo = __shfl(acc[c], (lane & 48) | ((col + m) & 15), 64);
-    if (col < m)
-      store_agent(part + (int64_t)col * p.d + r0 + 4 * (lane >> 4) + c, tagged(tag, __float_as_uint(__fadd_rn(acc[c], lo))));
+    if (col < m) {
+      const float v = __fadd_rn(acc[c], lo);
+      const int row = r0 + 4 * (lane >> 4) + c;
+      if (alone) {
+        const float o = __fadd_rn(0.0f, v);
+        if (p.out_f32) p.out_f32[(int64_t)col * p.d + row] = o;
+        if (p.out_bf16) p.out_bf16[(int64_t)col * p.d + row] = (uint16_t)f32_to_bf16_bits(o);
+      } else {
+        store_agent(part + (int64_t)col * p.d + row, tagged(tag, __float_as_uint(v)));
+      }
+    }
   }
   return state;
 }
@@ -822,6 +835,7 @@ __device__ __noinline__ void down_finish(uint64_t kernarg, int q_arg) {
   down_slot_of(p, q, is_shared, s, g, h);
   const int n_routed = sh.n_routed;
   if (!is_shared && s >= n_routed) return;
+  if (n_routed == 1 && !p.shared) return;  // the down item wrote its rows itself
   int last = n_routed > 0 ? down_index(p, n_routed - 1, g) : -1;
   if (p.shared && p.sd0 + 2 * g + 1 > last) last = p.sd0 + 2 * g + 1;
   if (q != last) return;

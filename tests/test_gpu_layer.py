@@ -267,3 +267,21 @@ def test_routed_layer_token_table_is_hash_routing(layer, dev):
     torch.cuda.synchronize()
     assert torch.equal(one[1], f1)
     assert ops.moe_layer_status(dev) == 0
+
+
+@pytest.mark.parametrize("ids", [[[17]], [[17], [17]], [[-1], [40]], [[40, -1, 40]]])
+def test_routed_layer_one_slot_alone(layer, dev, ids):
+    """One routed slot and no shared expert: the down items write their rows
+    themselves (no row-group sum); bit-identical to moe_decode in fp32 and
+    bf16, also with two tokens on the slot and with repeated / invalid ids."""
+    store, _, _ = layer
+    idx = torch.tensor(ids, dtype=torch.int64, device=dev)
+    m, k = idx.shape
+    x = synthetic.hidden(SEED, 950 + m * k, m, D, dev)
+    w = torch.rand(m, k, generator=torch.Generator().manual_seed(m * k)).to(dev)
+    a = routed(x, idx, store.table(0), None, w=w, k=k)
+    f32 = torch.empty(m, D, dtype=torch.float32, device=dev)
+    b16, _ = ops.moe_decode(x, idx, w, store.table(0), ops.SCALE_E8M0, None, 10.0, out_f32=f32, d=D, i=I)
+    torch.cuda.synchronize()
+    assert ops.moe_layer_status(dev) == 0
+    assert torch.equal(a[1], f32) and torch.equal(a[0], b16)
