@@ -291,6 +291,9 @@ def run_headline(torch, args, lb: LayerBench, cpu_info):
     t0 = time.perf_counter()
     total_ms, samples = timed_launches(torch, lb.stream, step, L, args.steps, args.warmup)
     wall = time.perf_counter() - t0
+    # after the timed region: the same rotation replayed 100 times, a larger
+    # sample of the per-launch time (reported beside the timed one, not used for value)
+    _, long_samples = timed_launches(torch, lb.stream, step, L, 100 * L, L)
     ops.check_moe_layer_status(dev)
     sp = spread(samples)
     us = sp["median_us"]
@@ -353,6 +356,9 @@ def run_headline(torch, args, lb: LayerBench, cpu_info):
         "timing": {**sp, "mean_us": round(total_ms * 1e3 / args.steps, 3), "timed_ms": round(total_ms, 3),
                    "method": "HIP events around each graph replay (rotation of --layers launches, remainder graph "
                              "for --steps % --layers); value and ms_per_step from the median"},
+        "timing_check": {**spread(long_samples), "launches": 100 * L,
+                         "method": "after the timed region, 100 replays of the same rotation graph (not used for "
+                                   "value)"},
         "layer_status": 0,
         "pct_hbm_peak": round(100.0 * routed_gbs / HBM_PEAK_GBS, 2),
         "expert_gbs": round(EXPERT_WEIGHT_BYTES / (us * 1e-6) / 1e9, 1),
