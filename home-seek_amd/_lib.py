@@ -27,6 +27,14 @@ _f32 = ctypes.c_float
 _u64 = ctypes.c_uint64
 _size = ctypes.c_size_t
 
+
+
+class NormTail(ctypes.Structure):
+    """hsmoe_norm_tail: the next layer's residual adds + RMSNorm ending a layer launch."""
+    _fields_ = [("h_dev", _c_void_p), ("residual_dev", _c_void_p), ("weight_dev", _c_void_p), ("eps", _f32),
+                ("h_out_dev", _c_void_p), ("norm_out_dev", _c_void_p)]
+
+
 # name -> (restype, argtypes); mirrors include/hsmoe.h
 _SIGNATURES = {
     "hsmoe_version": (_int, []),
@@ -54,6 +62,12 @@ _SIGNATURES = {
     "hsmoe_moe_layer_decode_routed": (_int, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _f32,
                                              _int, _c_void_p, _i64, _int, _c_void_p, _f32, _c_void_p, _c_void_p,
                                              _c_void_p, _size, _c_void_p]),
+    "hsmoe_moe_layer_decode_norm": (_int, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _i64, _int, _f32,
+                                           _c_void_p, _int, _c_void_p, _f32, _c_void_p, _c_void_p, _c_void_p,
+                                           _c_void_p, _c_void_p, _c_void_p, _c_void_p, _size, _c_void_p]),
+    "hsmoe_moe_layer_decode_routed_norm": (_int, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _i64,
+                                                  _c_void_p, _f32, _int, _c_void_p, _i64, _int, _c_void_p, _f32,
+                                                  _c_void_p, _c_void_p, _c_void_p, _c_void_p, _size, _c_void_p]),
     "hsmoe_moe_layer_decode_noalloc": (_int, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _i64, _int, _f32,
                                               _c_void_p, _int, _c_void_p, _f32, _c_void_p, _c_void_p, _c_void_p,
                                               _c_void_p, _c_void_p, _c_void_p, _c_void_p]),

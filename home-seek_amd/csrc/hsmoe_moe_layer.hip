@@ -34,6 +34,10 @@
 // of its slot has published the slot's activations, then stages them in LDS.
 // The last down item of a row group adds the slots' partials in slot order
 // (routed ascending, shared last) and writes the output rows.
+// With a norm tail (the _norm entry points) m more items come last, one per
+// token row: the next layer's residual adds and RMSNorm of this layer's
+// output, from the rows the row-group sums also publish as tagged words
+// (see tail_item).
 // Workgroup b runs items b, b + G, b + 2G, ... with G no larger than the
 // number of workgroups the GPU holds at once, so every item a workgroup waits
 // for is held by a running workgroup.  Every wait is bounded; a wait that
@@ -43,6 +47,7 @@
 
 #include "hsmoe_common.h"
 #include "hsmoe_internal.h"
+#include "hsmoe_norm.h"
 #include "hsmoe_route.h"
 #include "hsmoe_tiles.h"
 
@@ -72,6 +77,7 @@ constexpr int kWaitAct = 4609;     //   a down item's wait for its slot's activa
 constexpr int kWaitShared = 4610;  //   the shared down's wait for the shared activations
 constexpr int kWaitPart = 4611;    //   a row group's wait for the slots' partials
 constexpr int kWaitGate = 4612;    //   a shared up item's wait for its rows' gate sums
+constexpr int kWaitTail = 4613;    //   a tail item's wait for its output row
 constexpr int kMaxRowGroups = 2048;
 constexpr size_t kCtlBytes = 4096;
 // Once a launch's tag reaches kRearmTag its last workgroup zeroes the tagged
@@ -103,6 +109,7 @@ struct LayerParams {
   uint64_t* act;   // tagged [S][m][i] weighted activations of the routed slots
   uint64_t* sgh;   // tagged [2][m][i] shared expert gate row sums (0) and activations (1)
   uint64_t* part;  // tagged [S + 1][m][d] per-slot down partials (slot S: shared)
+  uint64_t* fin;   // tagged [m][d] output rows for the tail items, or null (no tail)
   uint4* wipe;      // the workspace after the control words, zeroed at a re-arm
   int64_t wipe_n;   //   (16-byte units)
   unsigned* status_out;  // or null: receives this launch's status, the sticky word is cleared
@@ -114,9 +121,16 @@ struct LayerParams {
   const float* route_w;
   float route_wconst;
   int64_t route_rows;
+  // norm tail (tail_w set): h_out = bf16(bf16(h + bf16(out)) + res), norm_out = RMSNorm(h_out) * w
+  const uint16_t* tail_h;    // bf16 [m, d]
+  const uint16_t* tail_res;  // bf16 [d] or null
+  const uint16_t* tail_w;    // bf16 [d] or null: no tail
+  uint16_t* tail_h_out;      // bf16 [m, d] (may be tail_h)
+  uint16_t* tail_out;        // bf16 [m, d]
+  float tail_eps;
   // item ranges [start, end): R is [0, n_router); the others follow in an
   // order where every item's producers come before it
-  int n_router, sgu0, sgu1, sd0, sd1, gu0, gu1, d0, d1, n_items;
+  int n_router, sgu0, sgu1, sd0, sd1, gu0, gu1, d0, d1, n_main, n_items;  // tail items: [n_main, n_items)
   // routed down items in pairs (drun = 2; else 1): in each block of 2 * dgrid
   // items, dk slots whose row groups a workgroup takes two at a time, so
   // that its second item reuses the staged activations of its first
@@ -379,6 +393,19 @@ __device__ __forceinline__ LayerParams params(uint64_t kernarg) {
   return *(KernargParams*)(((uint64_t)hi << 32) | lo);
 #else
   return LayerParams{};  // host pass: never called
+#endif
+}
+
+// p.fin, loaded from the kernarg segment where it is used (a volatile load
+// the compiler cannot hoist): held across down_finish's polls, the pointer
+// made that function save a callee-saved register to scratch.
+__device__ __forceinline__ uint64_t* fin_late(uint64_t kernarg) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)kernarg);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(kernarg >> 32));
+#if defined(__HIP_DEVICE_COMPILE__)
+  return ((const volatile KernargParams*)(((uint64_t)hi << 32) | lo))->fin;
+#else
+  return nullptr;
 #endif
 }
 
@@ -813,6 +840,7 @@ __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg
         const float o = __fadd_rn(0.0f, v);
         if (p.out_f32) p.out_f32[(int64_t)col * p.d + row] = o;
         if (p.out_bf16) p.out_bf16[(int64_t)col * p.d + row] = (uint16_t)f32_to_bf16_bits(o);
+        if (p.fin) store_agent(p.fin + (int64_t)col * p.d + row, tagged(tag, __float_as_uint(o)));
       } else {
         store_agent(part + (int64_t)col * p.d + row, tagged(tag, __float_as_uint(v)));
       }
@@ -864,7 +892,97 @@ __device__ __noinline__ void down_finish(uint64_t kernarg, int q_arg) {
       const int64_t o = (int64_t)t * p.d + dd;
       if (p.out_f32) p.out_f32[o] = v;
       if (p.out_bf16) p.out_bf16[o] = (uint16_t)f32_to_bf16_bits(v);
+      uint64_t* const fin = fin_late(kernarg);
+      if (fin) store_agent(fin + o, tagged(tag, __float_as_uint(v)));
     }
+  }
+}
+
+// Tail item of token row t (launches with a norm tail; the slot plan exists):
+// the next layer's input from this layer's output row,
+//   h_out = bf16(bf16(h + bf16(out)) + res),  norm_out = RMSNorm(h_out) * w,
+// with the arithmetic and the order of hsmoe_add_rms_norm (hsmoe_norm.h):
+// this thread's 8-column chunks c = tid, tid + 256, ... in turn, the wave's
+// butterfly, the waves in order -- bit-identical to the layer's bf16 output
+// followed by hsmoe_add_rms_norm.  The output row comes from the tagged words
+// the row-group sums (or a lone slot's down items) publish; two chunks' 16
+// words are polled with every load in flight at once.  A layer with no expert
+// to run has a zero output and nothing to wait for.
+__device__ __noinline__ void tail_item(uint64_t kernarg, int t_arg) {
+  const int t = __builtin_amdgcn_readfirstlane(t_arg);
+  const LayerParams p = params(kernarg);
+  const unsigned tag = launch_tag(p.ctl);
+  const bool zero = g_sh.n_routed == 0 && !p.shared;
+  const int tid = (int)threadIdx.x;
+  const int chunks = p.d / 8;  // d <= 8192: at most 4 chunks per thread
+  const int64_t base = (int64_t)t * chunks;
+  const uint4* h = (const uint4*)p.tail_h + base;
+  const uint4* res = (const uint4*)p.tail_res;
+  const uint4* w = (const uint4*)p.tail_w;
+  const uint64_t* fin = p.fin + (int64_t)t * p.d;
+  uint4 u[4], wv[4];
+  float s = 0.0f;
+#pragma unroll
+  for (int b0 = 0; b0 < 4; b0 += 2) {
+    uint4 hv[2], rv[2];
+    unsigned need = 0;
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      const int c = tid + kThreads * (b0 + bb);
+      hv[bb] = rv[bb] = wv[b0 + bb] = make_uint4(0u, 0u, 0u, 0u);
+      if (c < chunks) {
+        hv[bb] = h[c];
+        if (res) rv[bb] = res[c];
+        wv[b0 + bb] = w[c];
+        if (!zero) need |= 0xffu << (8 * bb);
+      }
+    }
+    float f[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) f[j] = 0.0f;
+    for (unsigned it = 0; it < kSpinLimit; ++it) {
+      const unsigned cur = need;
+      uint64_t wd[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        wd[j] = (cur >> j) & 1u ? load_agent(fin + 8 * (tid + kThreads * (b0 + (j >> 3))) + (j & 7)) : 0ull;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (((cur >> j) & 1u) && (unsigned)(wd[j] >> 32) == tag) {
+          f[j] = __uint_as_float((unsigned)wd[j]);
+          need &= ~(1u << j);
+        }
+      if (__ballot(need != 0) == 0) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (need) store_agent(p.ctl + kCtlErr, 1u + (unsigned)kWaitTail);
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      const int c = tid + kThreads * (b0 + bb);
+      const float* fb = f + 8 * bb;
+      const uint4 a = make_uint4(f32_to_bf16_bits(fb[0]) | (f32_to_bf16_bits(fb[1]) << 16),
+                                 f32_to_bf16_bits(fb[2]) | (f32_to_bf16_bits(fb[3]) << 16),
+                                 f32_to_bf16_bits(fb[4]) | (f32_to_bf16_bits(fb[5]) << 16),
+                                 f32_to_bf16_bits(fb[6]) | (f32_to_bf16_bits(fb[7]) << 16));
+      uint4 x = norm_add_chunk(hv[bb], a);
+      if (res) x = norm_add_chunk(x, rv[bb]);
+      u[b0 + bb] = x;
+      if (c < chunks) {
+        ((uint4*)p.tail_h_out)[base + c] = x;
+        s = norm_sumsq_chunk(x, s);
+      }
+    }
+  }
+  s = norm_wave_sum(s);
+  float* const part = &g_sh.red[0][0][0];  // free: every item starts after a barrier
+  if ((tid & 63) == 0) part[tid >> 6] = s;
+  __syncthreads();
+  const float inv = norm_inv(part, p.d, p.tail_eps);
+  uint4* const out = (uint4*)p.tail_out + base;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int c = tid + kThreads * b;
+    if (c < chunks) out[c] = norm_scale_chunk(u[b], wv[b], inv);
   }
 }
 
@@ -873,8 +991,9 @@ __global__ void __launch_bounds__(kThreads, 2) moe_layer_kernel(LayerParams p) {
   if (threadIdx.x == 0) g_sh.have_plan = 0;
   if (p.shared && threadIdx.x < 6) g_sh.ent[p.S][threadIdx.x] = ldg<uint64_t>(p.shared + threadIdx.x);
   const uint64_t kernarg = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();  // &p
-  const int n_items = p.n_items, n_router = p.n_router;
-  for (int q = blockIdx.x; q < n_items; q += gridDim.x) {
+  const int n_main = p.n_main, n_router = p.n_router;
+  int q = blockIdx.x;
+  for (; q < n_main; q += gridDim.x) {
     __syncthreads();  // the previous item's readers of the LDS scratch are done
     if (q < n_router) {
       state = router_item(kernarg, q, state);
@@ -908,6 +1027,11 @@ __global__ void __launch_bounds__(kThreads, 2) moe_layer_kernel(LayerParams p) {
       state = down_item<false>(kernarg, q, state);
       down_finish(kernarg, q);
     }
+  }
+  for (; q < p.n_items; q += gridDim.x) {  // norm tail items, last in the order
+    __syncthreads();
+    if (!g_sh.have_plan) plan_item(kernarg);
+    tail_item(kernarg, q - p.n_main);
   }
   __syncthreads();
   // the routing outputs come from the last workgroup, also when it ran no item
@@ -945,7 +1069,8 @@ size_t layer_lds(int64_t m, int64_t d, int64_t i) { return (size_t)(m * d > 2 * 
 int64_t score_stride_words(int64_t m, int64_t n_exp) { return (m * n_exp * 8 + 4095) / 4096 * 512; }
 size_t scores_bytes(int64_t m, int64_t n_exp) { return (size_t)kScoreCopies * score_stride_words(m, n_exp) * 8; }
 size_t act_bytes(int64_t m, int64_t i, int top_k) { return align256((size_t)(m * top_k + 2) * m * i * 8); }
-size_t part_bytes(int64_t m, int64_t d, int top_k) { return align256((size_t)(m * top_k + 1) * m * d * 8); }
+// partials of the m * top_k routed slots and the shared one, then the output rows (fin)
+size_t part_bytes(int64_t m, int64_t d, int top_k) { return align256((size_t)(m * top_k + 2) * m * d * 8); }
 
 // Workgroups of moe_layer_kernel the device holds at once, for an LDS size.
 int resident_workgroups(size_t lds, int* out) {
@@ -996,8 +1121,9 @@ namespace {
 int check_layer_args(const char* name, const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
                      int64_t n_experts, int top_k, const uint64_t* expert_table, int scale_kind,
                      const int64_t* topk_idx_out, const float* topk_w_out, const float* out_f32,
-                     const void* out_bf16, bool given_route = false) {
-  if (!x || !expert_table || (!out_f32 && !out_bf16) || (!given_route && (!gate_w || !topk_idx_out || !topk_w_out)))
+                     const void* out_bf16, bool given_route = false, bool tail = false) {
+  if (!x || !expert_table || (!tail && !out_f32 && !out_bf16) ||
+      (!given_route && (!gate_w || !topk_idx_out || !topk_w_out)))
     return fail(HSMOE_ERR_ARG, "%s: null pointer or no output", name);
   if (scale_kind != HSMOE_SCALE_E8M0 && scale_kind != HSMOE_SCALE_F32)
     return fail(HSMOE_ERR_ARG, "%s: unknown scale_kind %d", name, scale_kind);
@@ -1030,9 +1156,15 @@ int launch_layer(const char* name, const void* x, int64_t m, int64_t d, int64_t 
                  const uint64_t* expert_table, int scale_kind, const uint64_t* shared, float swiglu_limit,
                  int64_t* topk_idx_out, float* topk_w_out, void* logits_out, float* out_f32, void* out_bf16,
                  void* workspace, size_t workspace_bytes, unsigned* status_out, hipStream_t stream,
-                 const GivenRoute* route = nullptr) {
+                 const GivenRoute* route = nullptr, const hsmoe_norm_tail* tail = nullptr) {
   const size_t lds = layer_lds(m, d, i);
   LayerParams p;
+  p.tail_h = tail ? (const uint16_t*)tail->h_dev : nullptr;
+  p.tail_res = tail ? (const uint16_t*)tail->residual_dev : nullptr;
+  p.tail_w = tail ? (const uint16_t*)tail->weight_dev : nullptr;
+  p.tail_h_out = tail ? (uint16_t*)tail->h_out_dev : nullptr;
+  p.tail_out = tail ? (uint16_t*)tail->norm_out_dev : nullptr;
+  p.tail_eps = tail ? tail->eps : 0.0f;
   p.route_idx = route ? route->idx : nullptr;
   p.route_tok = route ? route->tok : nullptr;
   p.route_rows = route ? route->rows : 0;
@@ -1067,6 +1199,7 @@ int launch_layer(const char* name, const void* x, int64_t m, int64_t d, int64_t 
   p.sgh = p.act + (size_t)p.S * m * i;
   ws += act_bytes(m, i, top_k);
   p.part = (uint64_t*)ws;
+  p.fin = tail ? p.part + (size_t)(p.S + 1) * m * d : nullptr;
   p.wipe = (uint4*)((char*)workspace + kCtlBytes);
   p.wipe_n = (int64_t)((workspace_bytes - kCtlBytes) / 16);
   p.status_out = status_out;
@@ -1098,7 +1231,8 @@ int launch_layer(const char* name, const void* x, int64_t m, int64_t d, int64_t 
     p.d0 = p.gu1;
     p.d1 = p.d0 + n_d;
   }
-  p.n_items = p.sgu1 + n_sd + n_gu + n_d;
+  p.n_main = p.sgu1 + n_sd + n_gu + n_d;
+  p.n_items = p.n_main + (tail ? (int)m : 0);
   int resident = 0;
   int rc = resident_workgroups(lds, &resident);
   if (rc) return rc;
@@ -1161,6 +1295,76 @@ extern "C" int hsmoe_moe_layer_decode_routed(const void* x, int64_t m, int64_t d
   return launch_layer(name, x, m, d, i, nullptr, nullptr, n_experts, top_k, 1.0f, expert_table, scale_kind, shared,
                       swiglu_limit, nullptr, nullptr, nullptr, out_f32, out_bf16, workspace, workspace_bytes, nullptr,
                       (hipStream_t)stream, &route);
+}
+
+namespace {
+
+// Checks a norm tail of m rows of d (its h_out may be its h; norm_out must not
+// overlap x, h, residual or weight).
+int check_tail(const char* name, const hsmoe_norm_tail* tail, const void* x, int64_t m, int64_t d) {
+  if (!tail || !tail->h_dev || !tail->weight_dev || !tail->h_out_dev || !tail->norm_out_dev)
+    return fail(HSMOE_ERR_ARG, "%s: the norm tail needs h, weight, h_out and norm_out", name);
+  if (!aligned(tail->h_dev, 16) || !aligned(tail->weight_dev, 16) || !aligned(tail->h_out_dev, 16) ||
+      !aligned(tail->norm_out_dev, 16) || (tail->residual_dev && !aligned(tail->residual_dev, 16)))
+    return fail(HSMOE_ERR_SHAPE, "%s: norm tail rows must be 16-byte aligned", name);
+  if (!(tail->eps >= 0.0f)) return fail(HSMOE_ERR_ARG, "%s: norm tail eps must be >= 0", name);
+  const size_t rows = (size_t)m * d * 2, row = (size_t)d * 2;
+  auto overlap = [](const void* a, size_t na, const void* b, size_t nb) {
+    const char *pa = (const char*)a, *pb = (const char*)b;
+    return b && pa < pb + nb && pb < pa + na;
+  };
+  const void* out = tail->norm_out_dev;
+  if (overlap(out, rows, x, rows) || overlap(out, rows, tail->h_dev, rows) ||
+      overlap(out, rows, tail->h_out_dev, rows) || overlap(out, rows, tail->residual_dev, row) ||
+      overlap(out, rows, tail->weight_dev, row) ||
+      (tail->h_out_dev != tail->h_dev && overlap(tail->h_out_dev, rows, tail->h_dev, rows)))
+    return fail(HSMOE_ERR_ARG, "%s: norm_out overlaps another operand (or h_out partly overlaps h)", name);
+  return HSMOE_OK;
+}
+
+}  // namespace
+
+extern "C" int hsmoe_moe_layer_decode_norm(const void* x, int64_t m, int64_t d, int64_t i, const void* gate_w,
+                                           const float* gate_bias, int64_t n_experts, int top_k,
+                                           float routed_scaling, const uint64_t* expert_table, int scale_kind,
+                                           const uint64_t* shared, float swiglu_limit, int64_t* topk_idx_out,
+                                           float* topk_w_out, void* logits_out, float* out_f32, void* out_bf16,
+                                           const hsmoe_norm_tail* tail, void* workspace, size_t workspace_bytes,
+                                           hsmoe_stream_t stream) {
+  const char* name = "hsmoe_moe_layer_decode_norm";
+  int rc = check_layer_args(name, x, m, d, i, gate_w, n_experts, top_k, expert_table, scale_kind, topk_idx_out,
+                            topk_w_out, out_f32, out_bf16, false, true);
+  if (rc) return rc;
+  if ((rc = check_tail(name, tail, x, m, d))) return rc;
+  const size_t need = hsmoe_moe_layer_workspace_size(m, d, i, n_experts, top_k);
+  if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+    return fail(HSMOE_ERR_WORKSPACE, "%s: zero-filled workspace of %zu bytes (256-byte aligned) needed", name, need);
+  return launch_layer(name, x, m, d, i, gate_w, gate_bias, n_experts, top_k, routed_scaling, expert_table,
+                      scale_kind, shared, swiglu_limit, topk_idx_out, topk_w_out, logits_out, out_f32, out_bf16,
+                      workspace, workspace_bytes, nullptr, (hipStream_t)stream, nullptr, tail);
+}
+
+extern "C" int hsmoe_moe_layer_decode_routed_norm(const void* x, int64_t m, int64_t d, int64_t i,
+                                                  const int64_t* topk_idx, const int64_t* token_ids,
+                                                  int64_t table_rows, const float* topk_w, float weight_all,
+                                                  int top_k, const uint64_t* expert_table, int64_t n_experts,
+                                                  int scale_kind, const uint64_t* shared, float swiglu_limit,
+                                                  float* out_f32, void* out_bf16, const hsmoe_norm_tail* tail,
+                                                  void* workspace, size_t workspace_bytes, hsmoe_stream_t stream) {
+  const char* name = "hsmoe_moe_layer_decode_routed_norm";
+  if (!topk_idx) return fail(HSMOE_ERR_ARG, "%s: null topk_idx", name);
+  if (token_ids && table_rows < 1) return fail(HSMOE_ERR_ARG, "%s: a token table needs table_rows >= 1", name);
+  int rc = check_layer_args(name, x, m, d, i, nullptr, n_experts, top_k, expert_table, scale_kind, nullptr, nullptr,
+                            out_f32, out_bf16, true, true);
+  if (rc) return rc;
+  if ((rc = check_tail(name, tail, x, m, d))) return rc;
+  const size_t need = hsmoe_moe_layer_workspace_size(m, d, i, n_experts, top_k);
+  if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+    return fail(HSMOE_ERR_WORKSPACE, "%s: zero-filled workspace of %zu bytes (256-byte aligned) needed", name, need);
+  const GivenRoute route{topk_idx, token_ids, token_ids ? table_rows : 0, topk_w, weight_all};
+  return launch_layer(name, x, m, d, i, nullptr, nullptr, n_experts, top_k, 1.0f, expert_table, scale_kind, shared,
+                      swiglu_limit, nullptr, nullptr, nullptr, out_f32, out_bf16, workspace, workspace_bytes, nullptr,
+                      (hipStream_t)stream, &route, tail);
 }
 
 // Scratch of hsmoe_moe_layer_decode_noalloc: the workspace of every call of

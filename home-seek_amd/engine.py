@@ -147,33 +147,11 @@ class HomeSeekMoEEngine:
         B, T, D = hidden_states.shape
         flat = hidden_states.reshape(B * T, D)
         hashed = layer_idx < self.config.num_hash_layers and tid2eid is not None and input_ids is not None
-        if (not hashed and B * T <= ops.MAX_DECODE_TOKENS and gate_w.shape[0] <= ops.MAX_LAYER_EXPERTS
-                and flat.dtype == torch.bfloat16 and gate_w.dtype == torch.bfloat16):
-            # router + routed + shared experts in one launch (hsmoe_moe_layer_decode)
-            out, _, idx, _ = ops.moe_layer_decode(
-                flat, gate_w, gate_bias, self.store.table(layer_idx), SCALE_E8M0, self.store.shared_entry(layer_idx),
-                self.config.moe_intermediate_size, self.config.num_experts_per_tok,
-                self.config.routed_scaling_factor, self.config.swiglu_limit, out_f32=out_f32,
-                out_bf16=torch.empty(B * T, D, dtype=torch.bfloat16, device=flat.device))
-            self._last_routed_idx = idx
-            return out.reshape(B, T, D).to(hidden_states.dtype), set()
+        out_bf16 = torch.empty(B * T, D, dtype=torch.bfloat16, device=flat.device)
+        if self._one_launch_layer(flat, lw, layer_idx, input_ids, out_f32=out_f32, out_bf16=out_bf16):
+            return out_bf16.reshape(B, T, D).to(hidden_states.dtype), set()
         k = self.config.num_experts_per_tok
         table = self.store.table(layer_idx)
-        if (hashed and B * T <= ops.MAX_DECODE_TOKENS and table.shape[0] <= ops.MAX_LAYER_EXPERTS
-                and flat.dtype == torch.bfloat16 and tid2eid.dtype == torch.int64 and tid2eid.is_contiguous()
-                and tid2eid.device == flat.device and input_ids.device == flat.device
-                and input_ids.dtype == torch.int64):
-            # hash ids (tid2eid[input_ids], weight 1/k, engine.py:1018-1023) looked up
-            # inside the one-launch layer kernel (hsmoe_moe_layer_decode_routed)
-            # a copy: a caller may rewrite its id buffer in place (GreedyDecoder does)
-            ids = input_ids.reshape(-1).clone()
-            out, _ = ops.moe_layer_decode_routed(
-                flat, tid2eid, table, SCALE_E8M0, self.store.shared_entry(layer_idx),
-                self.config.moe_intermediate_size, weight_all=1.0 / k, token_ids=ids, top_k=k,
-                swiglu_limit=self.config.swiglu_limit, out_f32=out_f32,
-                out_bf16=torch.empty(B * T, D, dtype=torch.bfloat16, device=flat.device))
-            self._last_routed_idx = (tid2eid, ids)
-            return out.reshape(B, T, D).to(hidden_states.dtype), set()
         if hashed:
             idx, w = self._compute_hash_experts(input_ids.to(hidden_states.device), layer_idx, tid2eid)
         else:
@@ -184,6 +162,65 @@ class HomeSeekMoEEngine:
         out = self._fused_moe.forward_table(flat, idx, w, table, SCALE_E8M0,
                                             self.store.shared_entry(layer_idx), out_f32=out_f32)
         return out.reshape(B, T, D).to(hidden_states.dtype), set()
+
+    def _one_launch_layer(self, flat: torch.Tensor, lw: dict, layer_idx: int, input_ids=None,
+                          out_f32: torch.Tensor | None = None, out_bf16: torch.Tensor | None = None,
+                          norm: ops.NormTail | None = None) -> bool:
+        """The layer's FFN on hidden rows flat [M, D] in one launch when it
+        applies (M <= 8, bf16, at most 256 experts): router + routed + shared
+        experts (hsmoe_moe_layer_decode), or on hash layers the token table
+        looked up in the launch (hsmoe_moe_layer_decode_routed); with `norm`
+        the launch also does the next layer's adds + RMSNorm.  -> False (and
+        nothing launched) when it does not apply."""
+        gate_w = lw.get("ffn.gate.weight")
+        if gate_w is None:
+            return False
+        tid2eid = lw.get("ffn.gate.tid2eid")
+        m = flat.shape[0]
+        hashed = layer_idx < self.config.num_hash_layers and tid2eid is not None and input_ids is not None
+        k = self.config.num_experts_per_tok
+        if (not hashed and m <= ops.MAX_DECODE_TOKENS and gate_w.shape[0] <= ops.MAX_LAYER_EXPERTS
+                and flat.dtype == torch.bfloat16 and gate_w.dtype == torch.bfloat16):
+            # router + routed + shared experts in one launch (hsmoe_moe_layer_decode)
+            _, _, idx, _ = ops.moe_layer_decode(
+                flat, gate_w, lw.get("ffn.gate.bias"), self.store.table(layer_idx), SCALE_E8M0,
+                self.store.shared_entry(layer_idx), self.config.moe_intermediate_size, k,
+                self.config.routed_scaling_factor, self.config.swiglu_limit, out_f32=out_f32, out_bf16=out_bf16,
+                norm=norm)
+            self._last_routed_idx = idx
+            return True
+        table = self.store.table(layer_idx)
+        if (hashed and m <= ops.MAX_DECODE_TOKENS and table.shape[0] <= ops.MAX_LAYER_EXPERTS
+                and flat.dtype == torch.bfloat16 and tid2eid.dtype == torch.int64 and tid2eid.is_contiguous()
+                and tid2eid.device == flat.device and input_ids.device == flat.device
+                and input_ids.dtype == torch.int64):
+            # hash ids (tid2eid[input_ids], weight 1/k, engine.py:1018-1023) looked up
+            # inside the one-launch layer kernel (hsmoe_moe_layer_decode_routed)
+            # a copy: a caller may rewrite its id buffer in place (GreedyDecoder does)
+            ids = input_ids.reshape(-1).clone()
+            ops.moe_layer_decode_routed(
+                flat, tid2eid, table, SCALE_E8M0, self.store.shared_entry(layer_idx),
+                self.config.moe_intermediate_size, weight_all=1.0 / k, token_ids=ids, top_k=k,
+                swiglu_limit=self.config.swiglu_limit, out_f32=out_f32, out_bf16=out_bf16, norm=norm)
+            self._last_routed_idx = (tid2eid, ids)
+            return True
+        return False
+
+    def _forward_ffn_norm(self, hn: torch.Tensor, lw: dict, layer_idx: int, input_ids, h: torch.Tensor,
+                          weight: torch.Tensor, residual: torch.Tensor | None = None):
+        """_forward_ffn of normed rows hn [B, T, D] followed by the next
+        layer's adds and RMSNorm, in one launch: -> (h + FFN (+ residual),
+        its RMSNorm) [B, T, D], bit-identical to _forward_ffn then add_rms_norm;
+        None (nothing launched) where the one-launch layer does not apply."""
+        B, T, D = hn.shape
+        flat = hn.reshape(B * T, D)
+        h2 = h.reshape(B * T, D)
+        if h2.dtype != torch.bfloat16 or not h2.is_contiguous():
+            return None
+        norm = ops.NormTail(h2, weight, residual, self.config.rms_norm_eps)
+        if not self._one_launch_layer(flat, lw, layer_idx, input_ids, norm=norm):
+            return None
+        return norm.h_out.reshape(B, T, D), norm.norm_out.reshape(B, T, D)
 
     # ------------------------------------------------------------ MTP verify
     def _snapshot_verify_state(self):
@@ -252,20 +289,35 @@ class HomeSeekMoEEngine:
         for _ in range(num_draft):
             e = rms_norm(self._embed(tok).reshape(1, D), mw["enorm.weight"], eps)
             h_in = rms_norm(h_prev.reshape(1, D), mw["hnorm.weight"], eps) + e
-            h_prev, _ = self._forward_layer(h_in.reshape(1, 1, D), mw["layer"], mw["layer_idx"], tok)
-            hf = rms_norm(h_prev.reshape(1, D), mw["norm.weight"], eps)
+            h_prev, hf = self._forward_layer_norm(h_in.reshape(1, 1, D), mw["layer"], mw["layer_idx"], tok,
+                                                  mw["norm.weight"])
             _, pred, _ = ops.lm_head_accept(hf, self.lm_head, None, want_logits=False)
             tok = pred.reshape(1, 1)
             drafts.append(tok)
         return torch.cat(drafts, dim=-1), num_draft
 
+    def _next_norm(self, layer_idx: int, final_norm: bool):
+        """(residual, norm weight) that follow layer layer_idx's FFN: the next
+        layer's attention stand-in and ffn_norm, or after the last layer the
+        final norm (no residual); None when no fused norm follows."""
+        if layer_idx + 1 < self.config.num_hidden_layers:
+            lw = self._get_layer_weights(layer_idx + 1)
+            w = lw.get("ffn_norm.weight")
+            return None if w is None else (lw.get("attn.residual"), w)
+        if final_norm and self.norm_weight is not None:
+            return None, self.norm_weight
+        return None
+
     def _forward_stack(self, ids: torch.Tensor, final_norm: bool = True):
         """Embed ids [1, T] and run every layer -> (last hidden [1, T, D], its
-        final RMSNorm [T, D] or None).  Same values as _forward_layer in a loop;
-        each layer's FFN output is added in the next layer's fused add + norm
-        launch (hsmoe_add_rms_norm), which also adds that layer's residual."""
+        final RMSNorm [T, D] or None).  Same values as _forward_layer in a loop:
+        where the one-launch layer applies, each layer launch ends with the
+        next layer's residual adds and RMSNorm (or the final norm); elsewhere
+        the FFN output is added in the next add + norm launch
+        (hsmoe_add_rms_norm), which also adds that layer's residual."""
         eps = self.config.rms_norm_eps
         h = self._embed(ids)
+        hn = None  # this layer's normed input, when the previous launch made it
         pending = None  # FFN output of the previous layer, not yet added
         for layer_idx in range(self.config.num_hidden_layers):
             lw = self._get_layer_weights(layer_idx)
@@ -275,10 +327,20 @@ class HomeSeekMoEEngine:
                     h, pending = h + pending, None
                 h, _ = self._forward_layer(h, lw, layer_idx, ids)
                 continue
-            h, hn = ops.add_rms_norm(h, norm_w, add=pending, residual=lw.get("attn.residual"), eps=eps,
-                                     want_sum=True)
+            if hn is None:
+                h, hn = ops.add_rms_norm(h, norm_w, add=pending, residual=lw.get("attn.residual"), eps=eps,
+                                         want_sum=True)
+                pending = None
+            nxt = self._next_norm(layer_idx, final_norm)
+            fused = None if nxt is None else self._forward_ffn_norm(hn, lw, layer_idx, ids, h, nxt[1], nxt[0])
+            if fused is not None:
+                h, hn = fused
+                continue
             pending, _ = self._forward_ffn(hn, lw, layer_idx, ids)
+            hn = None
         if final_norm and self.norm_weight is not None:
+            if hn is not None:  # the last layer's launch made the final norm
+                return h, hn.reshape(-1, h.shape[-1])
             h, hf = ops.add_rms_norm(h, self.norm_weight, add=pending, eps=eps, want_sum=True)
             return h, hf.reshape(-1, h.shape[-1])
         if pending is not None:
@@ -351,6 +413,23 @@ class HomeSeekMoEEngine:
             hn = h
         ffn_out, used = self._forward_ffn(hn, lw, layer_idx, input_ids)
         return h + ffn_out, used
+
+    def _forward_layer_norm(self, h: torch.Tensor, lw: dict, layer_idx: int, input_ids, weight: torch.Tensor):
+        """_forward_layer followed by an RMSNorm with `weight` -> (h [B, T, D],
+        normed [B*T, D]); the norm runs in the layer's launch where the
+        one-launch layer applies (same values)."""
+        norm_w = lw.get("ffn_norm.weight")
+        if norm_w is not None:
+            h1, hn = ops.add_rms_norm(h, norm_w, residual=lw.get("attn.residual"), eps=self.config.rms_norm_eps,
+                                      want_sum=True)
+            fused = self._forward_ffn_norm(hn, lw, layer_idx, input_ids, h1, weight)
+            if fused is not None:
+                return fused[0], fused[1].reshape(-1, h.shape[-1])
+            ffn_out, _ = self._forward_ffn(hn, lw, layer_idx, input_ids)
+            h_out = h1 + ffn_out
+        else:
+            h_out, _ = self._forward_layer(h, lw, layer_idx, input_ids)
+        return h_out, rms_norm(h_out.reshape(-1, h.shape[-1]), weight, self.config.rms_norm_eps)
 
 
 class GreedyDecoder:

@@ -7,6 +7,8 @@ zero, so stream-ordered calls can share them.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -14,7 +16,7 @@ from ._lib import SCALE_E8M0, SCALE_F32, check, lib, ptr, require_cuda, stream_p
 
 __all__ = [
     "SCALE_E8M0", "SCALE_F32", "scale_kind_of", "fp4_dequant_bf16", "fp8_dequant_bf16", "router_topk",
-    "moe_decode", "moe_layer_decode", "moe_layer_decode_routed", "moe_layer_status", "moe_layer_status_words",
+    "moe_decode", "moe_layer_decode", "moe_layer_decode_routed", "NormTail", "moe_layer_status", "moe_layer_status_words",
     "clear_moe_layer_status", "check_moe_layer_status", "lm_head_accept", "expert_table", "shared_entry",
     "dequant_blocked", "xor_checksum", "MAX_DECODE_TOKENS", "MAX_LAYER_EXPERTS",
 ]
@@ -266,13 +268,48 @@ def moe_decode_stage(stage: int, x: torch.Tensor, topk_idx: torch.Tensor, topk_w
     check(rc, f"moe_decode stage {stage}")
 
 
+class NormTail:
+    """The next layer's residual adds and RMSNorm, done at the end of a layer
+    launch (the _norm entry points): with out = the layer's output in bf16,
+    h_out = bf16(bf16(h + out) + residual) and norm_out = RMSNorm(h_out) *
+    weight, bit-identical to add_rms_norm(h, weight, add=out, residual=...).
+    h [M, D] bf16; residual [D] or None; weight [D]; the outputs are
+    allocated when not given (h_out may be h)."""
+
+    def __init__(self, h: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor | None = None,
+                 eps: float = 1e-6, h_out: torch.Tensor | None = None, norm_out: torch.Tensor | None = None):
+        require_cuda(h, weight, residual, h_out, norm_out)
+        if h.dtype != torch.bfloat16 or h.dim() != 2 or not h.is_contiguous():
+            raise ValueError("norm tail h must be a contiguous bf16 [M, D] tensor")
+        d = h.shape[1]
+        self.h = h
+        self.weight = weight.to(torch.bfloat16).reshape(-1).contiguous()
+        self.residual = None if residual is None else residual.to(torch.bfloat16).reshape(-1).contiguous()
+        if self.weight.numel() != d or (self.residual is not None and self.residual.numel() != d):
+            raise ValueError("norm tail weight and residual must be one row of the hidden size")
+        self.eps = float(eps)
+        self.h_out = torch.empty_like(h) if h_out is None else h_out
+        self.norm_out = torch.empty_like(h) if norm_out is None else norm_out
+        for t in (self.h_out, self.norm_out):
+            if t.shape != h.shape or t.dtype != torch.bfloat16 or not t.is_contiguous():
+                raise ValueError("norm tail outputs must be contiguous bf16 tensors shaped like h")
+
+    def struct(self, x: torch.Tensor) -> "_lib.NormTail":
+        if tuple(self.h.shape) != tuple(x.shape):
+            raise ValueError(f"norm tail rows {tuple(self.h.shape)} do not match the layer's {tuple(x.shape)}")
+        return _lib.NormTail(ptr(self.h), ptr(self.residual), ptr(self.weight), self.eps, ptr(self.h_out),
+                             ptr(self.norm_out))
+
+
 def moe_layer_decode(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor | None, table: torch.Tensor,
                      scale_kind: int, shared: torch.Tensor | None, i: int, top_k: int = 6, scaling: float = 1.5,
                      swiglu_limit: float = 10.0, out_bf16: torch.Tensor | None = None,
                      out_f32: torch.Tensor | None = None, idx_out: torch.Tensor | None = None,
-                     w_out: torch.Tensor | None = None, want_logits: bool = False):
+                     w_out: torch.Tensor | None = None, want_logits: bool = False, norm: NormTail | None = None):
     """Router + routed experts + shared expert of one layer for M <= 8 tokens in
-    one launch; returns (out_bf16, out_f32, idx, w[, logits]).
+    one launch; returns (out_bf16, out_f32, idx, w[, logits]).  With `norm`
+    the launch ends with its norm tail (norm.h_out, norm.norm_out receive
+    it) and no output is allocated unless asked for.
 
     Same results as router_topk followed by moe_decode.  Inputs must already be
     contiguous device tensors of the right dtypes when called inside a graph
@@ -296,16 +333,20 @@ def moe_layer_decode(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Ten
         w_out = torch.empty(m, top_k, dtype=torch.float32, device=dev)
     if tuple(idx_out.shape) != (m, top_k) or tuple(w_out.shape) != (m, top_k):
         raise ValueError("idx_out / w_out must be [M, top_k]")
-    if out_bf16 is None and out_f32 is None:
+    if out_bf16 is None and out_f32 is None and norm is None:
         out_bf16 = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
     logits = torch.empty(m, n_exp, dtype=torch.bfloat16, device=dev) if want_logits else None
     nbytes = lib().hsmoe_moe_layer_workspace_size(m, d, i, n_exp, top_k)
     ws = _workspace(dev, "layer", nbytes)
-    rc = lib().hsmoe_moe_layer_decode(ptr(x), m, d, i, ptr(gate_w), ptr(gate_bias), n_exp, top_k, scaling,
-                                      ptr(table), scale_kind, ptr(shared), swiglu_limit, ptr(idx_out), ptr(w_out),
-                                      ptr(logits), ptr(out_f32), ptr(out_bf16), ptr(ws), ws.numel(),
-                                      stream_ptr(dev))
-    check(rc, "hsmoe_moe_layer_decode")
+    args = (ptr(x), m, d, i, ptr(gate_w), ptr(gate_bias), n_exp, top_k, scaling, ptr(table), scale_kind, ptr(shared),
+            swiglu_limit, ptr(idx_out), ptr(w_out), ptr(logits), ptr(out_f32), ptr(out_bf16))
+    if norm is None:
+        rc = lib().hsmoe_moe_layer_decode(*args, ptr(ws), ws.numel(), stream_ptr(dev))
+        check(rc, "hsmoe_moe_layer_decode")
+    else:
+        tail = norm.struct(x)
+        rc = lib().hsmoe_moe_layer_decode_norm(*args, ctypes.addressof(tail), ptr(ws), ws.numel(), stream_ptr(dev))
+        check(rc, "hsmoe_moe_layer_decode_norm")
     res = (out_bf16, out_f32, idx_out, w_out)
     return res + (logits,) if want_logits else res
 
@@ -314,9 +355,10 @@ def moe_layer_decode_routed(x: torch.Tensor, topk_idx: torch.Tensor, table: torc
                             shared: torch.Tensor | None, i: int, topk_w: torch.Tensor | None = None,
                             weight_all: float = 1.0, token_ids: torch.Tensor | None = None, top_k: int | None = None,
                             swiglu_limit: float = 10.0, out_bf16: torch.Tensor | None = None,
-                            out_f32: torch.Tensor | None = None):
+                            out_f32: torch.Tensor | None = None, norm: NormTail | None = None):
     """Routed + shared experts of M <= 8 tokens in one launch with the routing
-    given (hsmoe_moe_layer_decode_routed); returns (out_bf16, out_f32).
+    given (hsmoe_moe_layer_decode_routed); returns (out_bf16, out_f32).  With
+    `norm` the launch ends with its norm tail, as in moe_layer_decode.
 
     token_ids None: topk_idx [M, k] are the ids.  Otherwise topk_idx is a
     token table [V, k] (a hash layer's tid2eid) and token t's ids are row
@@ -346,15 +388,20 @@ def moe_layer_decode_routed(x: torch.Tensor, topk_idx: torch.Tensor, table: torc
         topk_w = topk_w.to(torch.float32).contiguous()
         if topk_w.numel() != m * k:
             raise ValueError("topk_w must be [M, top_k]")
-    if out_bf16 is None and out_f32 is None:
+    if out_bf16 is None and out_f32 is None and norm is None:
         out_bf16 = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
     n_exp = table.shape[0]
     ws = _workspace(dev, "layer", lib().hsmoe_moe_layer_workspace_size(m, d, i, n_exp, k))
-    rc = lib().hsmoe_moe_layer_decode_routed(ptr(x), m, d, i, ptr(topk_idx), ptr(token_ids), rows, ptr(topk_w),
-                                             float(weight_all), k, ptr(table), n_exp, scale_kind, ptr(shared),
-                                             swiglu_limit, ptr(out_f32), ptr(out_bf16), ptr(ws), ws.numel(),
-                                             stream_ptr(dev))
-    check(rc, "hsmoe_moe_layer_decode_routed")
+    args = (ptr(x), m, d, i, ptr(topk_idx), ptr(token_ids), rows, ptr(topk_w), float(weight_all), k, ptr(table),
+            n_exp, scale_kind, ptr(shared), swiglu_limit, ptr(out_f32), ptr(out_bf16))
+    if norm is None:
+        rc = lib().hsmoe_moe_layer_decode_routed(*args, ptr(ws), ws.numel(), stream_ptr(dev))
+        check(rc, "hsmoe_moe_layer_decode_routed")
+    else:
+        tail = norm.struct(x)
+        rc = lib().hsmoe_moe_layer_decode_routed_norm(*args, ctypes.addressof(tail), ptr(ws), ws.numel(),
+                                                      stream_ptr(dev))
+        check(rc, "hsmoe_moe_layer_decode_routed_norm")
     return out_bf16, out_f32
 
 

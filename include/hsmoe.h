@@ -215,6 +215,45 @@ int hsmoe_moe_layer_decode_routed(const void* x_dev, int64_t m, int64_t d, int64
                                   void* out_bf16_dev, void* workspace_dev, size_t workspace_bytes,
                                   hsmoe_stream_t stream);
 
+/* The two one-launch layers above, ended by the next layer's residual adds
+ * and RMSNorm in the same launch (the "norm tail"), so that a stack of layers
+ * runs one launch per layer.  Replaces, after _forward_ffn, the residual add
+ * of the FFN output (reference src/home_seek/inference_engine/engine.py:2690)
+ * and the next layer's pre-FFN adds and rms_norm (engine.py:2653-2690,
+ * src/home_seek/utils.py:6-9), or the final norm after the last layer
+ * (engine.py:2480-2482).  With out = this layer's output rounded to bf16:
+ *   h_out    = bf16(bf16(h + out) + residual)   (no second add without residual)
+ *   norm_out = RMSNorm(h_out) * weight
+ * bit-identical to hsmoe_moe_layer_decode[_routed] with out_bf16 followed by
+ * hsmoe_add_rms_norm(h, out_bf16, residual, weight, m, d, eps, h_out,
+ * norm_out).  h, h_out, norm_out: bf16 [m, d]; residual: bf16 [d] or NULL;
+ * weight: bf16 [d]; h_out may be h; norm_out overlaps no other operand
+ * (x included).  out_f32 / out_bf16 may both be NULL here.  Other arguments,
+ * workspace and status word as in hsmoe_moe_layer_decode[_routed].
+ */
+typedef struct hsmoe_norm_tail {
+  const void* h_dev;
+  const void* residual_dev;
+  const void* weight_dev;
+  float eps;
+  void* h_out_dev;
+  void* norm_out_dev;
+} hsmoe_norm_tail;
+int hsmoe_moe_layer_decode_norm(const void* x_dev, int64_t m, int64_t d, int64_t i, const void* gate_w_dev,
+                                const float* gate_bias_dev, int64_t n_experts, int top_k, float routed_scaling,
+                                const uint64_t* expert_table_dev, int scale_kind, const uint64_t* shared_dev,
+                                float swiglu_limit, int64_t* topk_idx_out_dev, float* topk_w_out_dev,
+                                void* logits_out_dev, float* out_f32_dev, void* out_bf16_dev,
+                                const hsmoe_norm_tail* tail, void* workspace_dev, size_t workspace_bytes,
+                                hsmoe_stream_t stream);
+int hsmoe_moe_layer_decode_routed_norm(const void* x_dev, int64_t m, int64_t d, int64_t i,
+                                       const int64_t* topk_idx_dev, const int64_t* token_ids_dev, int64_t table_rows,
+                                       const float* topk_w_dev, float weight_all, int top_k,
+                                       const uint64_t* expert_table_dev, int64_t n_experts, int scale_kind,
+                                       const uint64_t* shared_dev, float swiglu_limit, float* out_f32_dev,
+                                       void* out_bf16_dev, const hsmoe_norm_tail* tail, void* workspace_dev,
+                                       size_t workspace_bytes, hsmoe_stream_t stream);
+
 /* hsmoe_moe_layer_decode without a workspace and without any allocation.
  * No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

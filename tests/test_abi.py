@@ -53,3 +53,23 @@ def test_layer_entry_point_rejects_bad_arguments():
                                   None, 4096, None, 4096, 64, None)
     assert rc == -4
     assert L.hsmoe_moe_layer_workspace_size(1, 4096, 2048, 256, 6) > 0
+
+
+def test_norm_tail_entry_points_check_the_tail():
+    """The _norm entry points check their norm tail before anything is launched."""
+    from home_seek_amd import _lib
+    L = _lib.lib()
+    args = (4096, 1, 4096, 2048, 4096, None, 256, 6, 1.5, 4096, 0, None, 10.0, 4096, 4096, None, None, None)
+    rc = L.hsmoe_moe_layer_decode_norm(*args, None, 4096, 1 << 24, None)
+    assert rc == -1 and b"norm tail" in L.hsmoe_last_error()
+    overlapping = _lib.NormTail(1 << 20, None, 1 << 21, 1e-6, 1 << 22, 4096)  # norm_out on x
+    rc = L.hsmoe_moe_layer_decode_norm(*args, ctypes.addressof(overlapping), 4096, 1 << 24, None)
+    assert rc == -1 and b"overlap" in L.hsmoe_last_error()
+    tail = _lib.NormTail(1 << 20, None, 1 << 21, 1e-6, 1 << 22, 1 << 23)
+    rc = L.hsmoe_moe_layer_decode_norm(*args, ctypes.addressof(tail), 4096, 64, None)
+    assert rc == -4
+    rc = L.hsmoe_moe_layer_decode_routed_norm(4096, 1, 4096, 2048, 4096, None, 0, None, 1.0, 6, 4096, 256, 0, None,
+                                              10.0, None, None, ctypes.addressof(overlapping), 4096, 1 << 24, None)
+    assert rc == -1 and b"overlap" in L.hsmoe_last_error()
+    rc = L.hsmoe_moe_layer_decode(*args, 4096, 1 << 24, None)  # without a tail an output is still required
+    assert rc == -1 and b"no output" in L.hsmoe_last_error()

@@ -186,8 +186,10 @@ def test_full_size_decode_step_teacher_forced(eng):
     """Every kernel call of one full-size decode step (the 43-layer M=1
     forward, the MTP block's two drafts, the T=3 verify of [A, d0, d1] and the
     four lm_head passes), checked against the oracle on the inputs the device
-    gave it: each fused residual add + RMSNorm (sum bit-exact, norm within one
-    bf16 step), each layer's FFN (expert ids bit-exact, output within one bf16
+    gave it: each residual add + RMSNorm, in its own launch or at the end of a
+    layer launch (sums bit-exact, norm within one bf16 step), each layer's FFN
+    (the same layer run without its norm tail: expert ids bit-exact, output
+    within one bf16
     step plus the 2e-2 bar), each lm_head pass (logits' argmax, accepted count
     and bonus row bit-exact), and the step's row built from those decisions.
     The synthetic stack cannot be compared free-running: its residual stream
@@ -200,6 +202,7 @@ def test_full_size_decode_step_teacher_forced(eng):
     from home_seek_amd.engine import GreedyDecoder
     calls = []
     inner_ffn, inner_norm, inner_head = eng._forward_ffn, ops.add_rms_norm, ops.lm_head_accept
+    inner_ffn_norm = eng._forward_ffn_norm
 
     def ffn(hn, lw, layer_idx, input_ids=None, out_f32=None):
         out, used = inner_ffn(hn, lw, layer_idx, input_ids, out_f32)
@@ -220,13 +223,25 @@ def test_full_size_decode_step_teacher_forced(eng):
                       res.cpu().tolist()))
         return lg, pred, res
 
-    eng._forward_ffn, ops.add_rms_norm, ops.lm_head_accept = ffn, norm, head
+    def ffn_norm(hn, lw, layer_idx, input_ids, h, weight, residual=None):
+        # the layer's FFN output from the same launch without its tail (the tail
+        # variant's own output is the same, bit for bit), then the fused launch
+        out, _ = ffn(hn, lw, layer_idx, input_ids)
+        fused = inner_ffn_norm(hn, lw, layer_idx, input_ids, h, weight, residual)
+        assert fused is not None
+        calls.append(("norm", np16(h), np16(out), None if residual is None else np16(residual.reshape(1, -1))[0],
+                      np16(weight.reshape(1, -1))[0], np16(fused[0]), np16(fused[1])))
+        calls.append(("tail",))
+        return fused
+
+    eng._forward_ffn, eng._forward_ffn_norm = ffn, ffn_norm
+    ops.add_rms_norm, ops.lm_head_accept = norm, head
     try:
         dec = GreedyDecoder(eng, 1, graph=False)
         dec.reset(31337)
         dec.run(1)
     finally:
-        del eng._forward_ffn
+        del eng._forward_ffn, eng._forward_ffn_norm
         ops.add_rms_norm, ops.lm_head_accept = inner_norm, inner_head
     row = dec.rows[0].cpu().tolist()
     assert ops.moe_layer_status(eng.device) == 0
@@ -234,6 +249,7 @@ def test_full_size_decode_step_teacher_forced(eng):
     so = StackOracle(SEED, NL, E, D, I, V, K, cache=False, workers=16)
     kinds = [c[0] for c in calls]
     assert kinds.count("ffn") == 2 * NL + 2 and kinds.count("head") == 4, kinds
+    assert kinds.count("tail") == 2 * NL + 2, kinds  # every layer launch ends with the next norm
     heads, worst = [], 0.0
     for c in calls:
         if c[0] == "norm":
@@ -250,7 +266,7 @@ def test_full_size_decode_step_teacher_forced(eng):
             g, r = orc.bf16_to_f32(out), orc.bf16_to_f32(orc.f32_to_bf16(f_ref))
             worst = max(worst, float(np.max(np.abs(g - r))))
             assert not np.any(np.abs(g - r) > np.abs(r) * 2.0 ** -7 + 2e-2), layer
-        else:
+        elif c[0] == "head":
             _, h, ids, pred, res = c
             lg = orc.logits_bf16(h, so.lm_head)
             assert pred == so.argmax(lg)
