@@ -80,6 +80,13 @@ _SIGNATURES = {
     "hsmoe_rms_norm": (_int, [_c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p, _c_void_p]),
     "hsmoe_add_rms_norm": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p,
                                   _c_void_p, _c_void_p]),
+    "hsmoe_embed_add_rms_norm": (_int, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _f32,
+                                        _c_void_p, _c_void_p, _c_void_p]),
+    "hsmoe_mtp_input": (_int, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                               _i64, _f32, _c_void_p, _c_void_p, _c_void_p]),
+    "hsmoe_decode_step_record": (_int, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
+                                        _c_void_p]),
     "hsmoe_xor_checksum_workspace_size": (_size, []),
     "hsmoe_xor_checksum": (_int, [_c_void_p, _i64, _c_void_p, _c_void_p, _size, _c_void_p]),
     "hsmoe_gen_bytes": (_int, [_u64, _i64, _c_void_p, _c_void_p]),

@@ -404,3 +404,71 @@ extern "C" int hsmoe_lm_head_accept(const void* h, const void* lm_head, int64_t 
     default: return launch<8>(w, hb, h64, d, vocab, ids, lg, pred_out, result_out, ws, st);
   }
 }
+
+namespace hsmoe {
+namespace {
+
+constexpr int kMaxDraftsRecorded = 15;
+
+// One decode step's emission at temperature 0 (engine.py:2862-2922), from the
+// verify's decisions: tokens = [a, d_0 .. d_{n-1}] (the verify's input ids),
+// pred = the verify's argmax per row, result = (n_accept, bonus_row):
+//   row   = [a, d_0 .. d_{n-1}, pred[bonus_row]]
+//   count = 1 + (n_accept > 0) * (n_accept + 1)   tokens emitted
+//   next  = pred[bonus_row] if n_accept > 0 else a
+// Without drafts (n = 0; pred, result unused): row = [a], count 1, next a.
+// Thread 0 writes the single-step outputs that are given and, with `rows`,
+// row k of rows [capacity][width] (width n + 2, or 1), counts[k] and
+// n_accepts[k], then *cur = next and *k = k + 1; a k outside [0, capacity)
+// writes no row.
+__global__ void __launch_bounds__(64)
+    step_record_kernel(const int64_t* tokens, int n, const int64_t* pred, const int64_t* result, int64_t* row_out,
+                       int64_t* count_out, int64_t* next_out, int64_t* nacc_out, int64_t* rows, int64_t* counts,
+                       int64_t* naccs, int64_t* k, int64_t capacity, int64_t* cur) {
+  if (threadIdx.x != 0) return;
+  const int64_t a = tokens[0];
+  int64_t nacc = 0, bonus = a;
+  if (n > 0) {
+    nacc = result[0];
+    const int64_t br = result[1] < 0 ? 0 : (result[1] > n ? n : result[1]);
+    bonus = pred[br];
+  }
+  const int width = n > 0 ? n + 2 : 1;
+  const int64_t count = nacc > 0 ? nacc + 2 : 1;
+  const int64_t next = nacc > 0 ? bonus : a;
+  const int64_t kk = rows ? *k : -1;
+  const bool keep = rows && kk >= 0 && kk < capacity;
+  for (int j = 0; j < width; ++j) {
+    const int64_t v = j == 0 ? a : (j <= n ? tokens[j] : bonus);
+    if (row_out) row_out[j] = v;
+    if (keep) rows[kk * width + j] = v;
+  }
+  if (count_out) *count_out = count;
+  if (next_out) *next_out = next;
+  if (nacc_out) *nacc_out = nacc;
+  if (keep) {
+    counts[kk] = count;
+    naccs[kk] = nacc;
+  }
+  if (rows) *k = kk + 1;
+  if (cur) *cur = next;
+}
+
+}  // namespace
+}  // namespace hsmoe
+
+extern "C" int hsmoe_decode_step_record(const int64_t* tokens, int64_t n_draft, const int64_t* pred,
+                                        const int64_t* result, int64_t* row_out, int64_t* count_out,
+                                        int64_t* next_out, int64_t* n_accept_out, int64_t* rows, int64_t* counts,
+                                        int64_t* n_accepts, int64_t* k, int64_t capacity, int64_t* cur,
+                                        hsmoe_stream_t stream) {
+  using namespace hsmoe;
+  if (!tokens || n_draft < 0 || n_draft > kMaxDraftsRecorded || (n_draft > 0 && (!pred || !result)))
+    return fail(HSMOE_ERR_ARG, "hsmoe_decode_step_record: tokens, 0 <= n_draft <= %d, and pred + result with drafts",
+                kMaxDraftsRecorded);
+  if (rows && (!counts || !n_accepts || !k || capacity < 1))
+    return fail(HSMOE_ERR_ARG, "hsmoe_decode_step_record: rows need counts, n_accepts, k and capacity >= 1");
+  hipLaunchKernelGGL(step_record_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, tokens, (int)n_draft, pred,
+                     result, row_out, count_out, next_out, n_accept_out, rows, counts, n_accepts, k, capacity, cur);
+  return check_launch("hsmoe_decode_step_record");
+}

@@ -165,12 +165,14 @@ class HomeSeekMoEEngine:
 
     def _one_launch_layer(self, flat: torch.Tensor, lw: dict, layer_idx: int, input_ids=None,
                           out_f32: torch.Tensor | None = None, out_bf16: torch.Tensor | None = None,
-                          norm: ops.NormTail | None = None) -> bool:
+                          norm: ops.NormTail | None = None, ids_owned: bool = False) -> bool:
         """The layer's FFN on hidden rows flat [M, D] in one launch when it
         applies (M <= 8, bf16, at most 256 experts): router + routed + shared
         experts (hsmoe_moe_layer_decode), or on hash layers the token table
         looked up in the launch (hsmoe_moe_layer_decode_routed); with `norm`
-        the launch also does the next layer's adds + RMSNorm.  -> False (and
+        the launch also does the next layer's adds + RMSNorm.  ids_owned: the
+        caller guarantees input_ids are not rewritten while _last_routed_idx
+        may still refer to them (no private copy is made).  -> False (and
         nothing launched) when it does not apply."""
         gate_w = lw.get("ffn.gate.weight")
         if gate_w is None:
@@ -196,8 +198,9 @@ class HomeSeekMoEEngine:
                 and input_ids.dtype == torch.int64):
             # hash ids (tid2eid[input_ids], weight 1/k, engine.py:1018-1023) looked up
             # inside the one-launch layer kernel (hsmoe_moe_layer_decode_routed)
-            # a copy: a caller may rewrite its id buffer in place (GreedyDecoder does)
-            ids = input_ids.reshape(-1).clone()
+            # a copy unless the caller owns the ids: a caller may rewrite its id
+            # buffer in place (GreedyDecoder does)
+            ids = input_ids.reshape(-1) if ids_owned else input_ids.reshape(-1).clone()
             ops.moe_layer_decode_routed(
                 flat, tid2eid, table, SCALE_E8M0, self.store.shared_entry(layer_idx),
                 self.config.moe_intermediate_size, weight_all=1.0 / k, token_ids=ids, top_k=k,
@@ -207,7 +210,7 @@ class HomeSeekMoEEngine:
         return False
 
     def _forward_ffn_norm(self, hn: torch.Tensor, lw: dict, layer_idx: int, input_ids, h: torch.Tensor,
-                          weight: torch.Tensor, residual: torch.Tensor | None = None):
+                          weight: torch.Tensor, residual: torch.Tensor | None = None, ids_owned: bool = False):
         """_forward_ffn of normed rows hn [B, T, D] followed by the next
         layer's adds and RMSNorm, in one launch: -> (h + FFN (+ residual),
         its RMSNorm) [B, T, D], bit-identical to _forward_ffn then add_rms_norm;
@@ -218,7 +221,7 @@ class HomeSeekMoEEngine:
         if h2.dtype != torch.bfloat16 or not h2.is_contiguous():
             return None
         norm = ops.NormTail(h2, weight, residual, self.config.rms_norm_eps)
-        if not self._one_launch_layer(flat, lw, layer_idx, input_ids, norm=norm):
+        if not self._one_launch_layer(flat, lw, layer_idx, input_ids, norm=norm, ids_owned=ids_owned):
             return None
         return norm.h_out.reshape(B, T, D), norm.norm_out.reshape(B, T, D)
 
@@ -272,29 +275,51 @@ class HomeSeekMoEEngine:
             raise RuntimeError("no embedding table: pass embed= or override _embed")
         return self.embed[ids].to(torch.bfloat16)
 
+    def _embed_fusable(self, ids: torch.Tensor) -> bool:
+        """The lookup can run inside the first norm's launch (hsmoe_embed_add_rms_norm /
+        hsmoe_mtp_input): this class's _embed on a bf16 [V, D] table on the ids' device."""
+        e = self.embed
+        return (type(self)._embed is HomeSeekMoEEngine._embed and e is not None and e.dtype == torch.bfloat16
+                and e.dim() == 2 and e.is_contiguous() and e.device == ids.device and ids.dtype == torch.int64)
+
     # ------------------------------------------------------------ MTP draft + decode loop
     @torch.no_grad()
     def _mtp_generate_draft(self, last_hidden: torch.Tensor, num_draft: int = 2, temperature: float = 0.0,
-                            last_token_id: torch.Tensor | None = None):
+                            last_token_id: torch.Tensor | None = None, out: torch.Tensor | None = None):
         """Greedy drafts from the MTP block (engine.py:2251-2339, stand-in described
-        in the module docstring) -> (draft_ids [1, n] int64, n); no host sync."""
+        in the module docstring) -> (draft_ids [1, n] int64, n); no host sync.
+        out (contiguous int64 [n], optional) is where the drafts are written."""
         mw = self._mtp_weights
-        if mw is None or self.embed is None or self.lm_head is None or last_token_id is None:
+        if mw is None or self.embed is None or self.lm_head is None or last_token_id is None or num_draft < 1:
             return None, 0
         eps = self.config.rms_norm_eps
         D = last_hidden.shape[-1]
+        if out is None:
+            out = torch.empty(num_draft, dtype=torch.int64, device=last_hidden.device)
         h_prev = last_hidden.reshape(1, 1, D)
         tok = last_token_id.reshape(1, 1)
-        drafts = []
-        for _ in range(num_draft):
-            e = rms_norm(self._embed(tok).reshape(1, D), mw["enorm.weight"], eps)
-            h_in = rms_norm(h_prev.reshape(1, D), mw["hnorm.weight"], eps) + e
-            h_prev, hf = self._forward_layer_norm(h_in.reshape(1, 1, D), mw["layer"], mw["layer_idx"], tok,
-                                                  mw["norm.weight"])
-            _, pred, _ = ops.lm_head_accept(hf, self.lm_head, None, want_logits=False)
-            tok = pred.reshape(1, 1)
-            drafts.append(tok)
-        return torch.cat(drafts, dim=-1), num_draft
+        lw = mw["layer"]
+        for j in range(num_draft):
+            if lw.get("ffn_norm.weight") is not None and self._embed_fusable(tok):
+                # embedding, enorm, hnorm, their sum, the residual add and ffn_norm in one launch
+                h1, hn = ops.mtp_input(tok, self.embed, h_prev, mw["enorm.weight"], mw["hnorm.weight"],
+                                       lw["ffn_norm.weight"], lw.get("attn.residual"), eps)
+                h1, hn = h1.reshape(1, 1, D), hn.reshape(1, 1, D)
+                fused = self._forward_ffn_norm(hn, lw, mw["layer_idx"], tok, h1, mw["norm.weight"], ids_owned=True)
+                if fused is not None:
+                    h_prev, hf = fused[0], fused[1].reshape(-1, D)
+                else:
+                    ffn_out, _ = self._forward_ffn(hn, lw, mw["layer_idx"], tok)
+                    h_prev = h1 + ffn_out
+                    hf = rms_norm(h_prev.reshape(-1, D), mw["norm.weight"], eps)
+            else:
+                e = rms_norm(self._embed(tok).reshape(1, D), mw["enorm.weight"], eps)
+                h_in = rms_norm(h_prev.reshape(1, D), mw["hnorm.weight"], eps) + e
+                h_prev, hf = self._forward_layer_norm(h_in.reshape(1, 1, D), lw, mw["layer_idx"], tok,
+                                                      mw["norm.weight"])
+            ops.lm_head_accept(hf, self.lm_head, None, want_logits=False, pred=out[j:j + 1])
+            tok = out[j:j + 1].reshape(1, 1)
+        return out[:num_draft].reshape(1, num_draft), num_draft
 
     def _next_norm(self, layer_idx: int, final_norm: bool):
         """(residual, norm weight) that follow layer layer_idx's FFN: the next
@@ -316,12 +341,22 @@ class HomeSeekMoEEngine:
         the FFN output is added in the next add + norm launch
         (hsmoe_add_rms_norm), which also adds that layer's residual."""
         eps = self.config.rms_norm_eps
-        h = self._embed(ids)
+        n_layers = self.config.num_hidden_layers
         hn = None  # this layer's normed input, when the previous launch made it
         pending = None  # FFN output of the previous layer, not yet added
-        for layer_idx in range(self.config.num_hidden_layers):
+        lw0 = self._get_layer_weights(0) if n_layers > 0 else {}
+        if lw0.get("ffn_norm.weight") is not None and self._embed_fusable(ids):
+            # lookup + first layer's residual add + RMSNorm in one launch
+            h, hn = ops.embed_add_rms_norm(ids, self.embed, lw0["ffn_norm.weight"], lw0.get("attn.residual"), eps)
+        else:
+            h = self._embed(ids)
+        for layer_idx in range(n_layers):
             lw = self._get_layer_weights(layer_idx)
             norm_w = lw.get("ffn_norm.weight")
+            # a hash layer keeps a private copy of the ids only when it is the
+            # last layer: otherwise a later layer replaces _last_routed_idx
+            # before this call returns
+            ids_owned = layer_idx + 1 < n_layers
             if norm_w is None:
                 if pending is not None:
                     h, pending = h + pending, None
@@ -332,7 +367,8 @@ class HomeSeekMoEEngine:
                                          want_sum=True)
                 pending = None
             nxt = self._next_norm(layer_idx, final_norm)
-            fused = None if nxt is None else self._forward_ffn_norm(hn, lw, layer_idx, ids, h, nxt[1], nxt[0])
+            fused = None if nxt is None else self._forward_ffn_norm(hn, lw, layer_idx, ids, h, nxt[1], nxt[0],
+                                                                    ids_owned=ids_owned)
             if fused is not None:
                 h, hn = fused
                 continue
@@ -354,7 +390,8 @@ class HomeSeekMoEEngine:
         return max(0, int(self.config.mtp_num_draft)) if has_mtp else 0
 
     @torch.no_grad()
-    def decode_step(self, cur: torch.Tensor, out_row: torch.Tensor | None = None):
+    def decode_step(self, cur: torch.Tensor, out_row: torch.Tensor | None = None, record: tuple | None = None,
+                    cur_out: torch.Tensor | None = None):
         """One greedy decode step, on the device only (engine.py:2809-2922 at
         temperature 0): M=1 forward of `cur` -> main token A; with n_draft =
         draft_count() > 0, drafts [d_0 .. d_{n_draft-1}] from the MTP block and
@@ -362,31 +399,33 @@ class HomeSeekMoEEngine:
         [2 + n_draft] = A, drafts, bonus token (row [1] = A without drafts);
         count of tokens emitted = 1 + (n > 0) * (n + 1); next token to forward
         (the bonus when n > 0, else A, which the next step forwards as the
-        reference's loop does); n), all device tensors."""
+        reference's loop does); n), all device tensors.  record = (rows, counts,
+        n_accepts, k) also stores the step as row k (advancing k on the device)
+        and cur_out receives the next token, in the step's last launch."""
         cur = cur.reshape(1, 1)
-        h, hf = self._forward_stack(cur)
-        _, pred, _ = ops.lm_head_accept(hf, self.lm_head, None, want_logits=False)
-        a = pred.reshape(1, 1)
         n_draft = self.draft_count()
+        toks = torch.empty(1 + n_draft, dtype=torch.int64, device=cur.device)  # [A, drafts]: the verify's ids
+        h, hf = self._forward_stack(cur)
+        ops.lm_head_accept(hf, self.lm_head, None, want_logits=False, pred=toks[:1])
         drafts = None
         if n_draft > 0:
-            drafts, n_draft = self._mtp_generate_draft(h, n_draft, 0.0, last_token_id=a)
+            own = (type(self)._mtp_generate_draft is HomeSeekMoEEngine._mtp_generate_draft
+                   and "_mtp_generate_draft" not in self.__dict__)
+            if own:  # the drafts go straight into the verify's id buffer
+                drafts, n_draft = self._mtp_generate_draft(h, n_draft, 0.0, last_token_id=toks[:1], out=toks[1:])
+            else:  # an override with the reference's signature
+                drafts, n_draft = self._mtp_generate_draft(h, n_draft, 0.0, last_token_id=toks[:1])
+                if drafts is not None and n_draft > 0:
+                    toks = torch.cat([toks[:1], drafts.reshape(-1)[:n_draft].to(torch.int64)])
         if drafts is None or n_draft == 0:
-            row = a.reshape(1)
-            if out_row is not None:
-                out_row.copy_(row)
-            one = torch.ones((), dtype=torch.int64, device=a.device)
-            return row, one, a.reshape(()), torch.zeros_like(one)
-        combined = torch.cat([a, drafts], dim=-1)
-        _, hfv = self._forward_stack(combined)
-        _, pred_v, result = ops.lm_head_accept(hfv, self.lm_head, combined.reshape(-1), want_logits=False)
-        n_acc = result[0]
-        bonus = pred_v.index_select(0, result[1:2]).reshape(())  # no host read of the row
-        row = torch.cat([a.reshape(1), drafts.reshape(-1), bonus.reshape(1)])
+            row, count, nxt, n_acc = ops.decode_step_record(toks[:1], record=record, cur=cur_out)
+        else:
+            toks = toks[:1 + n_draft]
+            _, hfv = self._forward_stack(toks.reshape(1, -1))
+            _, pred_v, result = ops.lm_head_accept(hfv, self.lm_head, toks, want_logits=False)
+            row, count, nxt, n_acc = ops.decode_step_record(toks, pred_v, result, record=record, cur=cur_out)
         if out_row is not None:
             out_row.copy_(row)
-        count = 1 + (n_acc > 0).to(torch.int64) * (n_acc + 1)
-        nxt = torch.where(n_acc > 0, bonus, a.reshape(()))
         return row, count, nxt, n_acc
 
     @torch.no_grad()
@@ -465,13 +504,8 @@ class GreedyDecoder:
             self.graph = g
 
     def _body(self):
-        row, count, nxt, n_acc = self.engine.decode_step(self.cur)
-        at = self.k.reshape(1)
-        self.rows.index_copy_(0, at, row.reshape(1, self.width))
-        self.counts.index_copy_(0, at, count.reshape(1))
-        self.n_accs.index_copy_(0, at, n_acc.reshape(1))
-        self.cur.copy_(nxt.reshape(1, 1))
-        self.k.add_(1)
+        # the step's last launch (hsmoe_decode_step_record) writes row k, advances k and sets cur
+        self.engine.decode_step(self.cur, record=(self.rows, self.counts, self.n_accs, self.k), cur_out=self.cur)
 
     def reset(self, first_id: int | None = None) -> None:
         """Rewinds the row index; first_id (if given) becomes the token to forward."""

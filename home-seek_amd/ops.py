@@ -18,7 +18,8 @@ __all__ = [
     "SCALE_E8M0", "SCALE_F32", "scale_kind_of", "fp4_dequant_bf16", "fp8_dequant_bf16", "router_topk",
     "moe_decode", "moe_layer_decode", "moe_layer_decode_routed", "NormTail", "moe_layer_status", "moe_layer_status_words",
     "clear_moe_layer_status", "check_moe_layer_status", "lm_head_accept", "expert_table", "shared_entry",
-    "dequant_blocked", "xor_checksum", "MAX_DECODE_TOKENS", "MAX_LAYER_EXPERTS",
+    "dequant_blocked", "xor_checksum", "MAX_DECODE_TOKENS", "MAX_LAYER_EXPERTS", "embed_add_rms_norm", "mtp_input",
+    "decode_step_record",
 ]
 
 MAX_DECODE_TOKENS = 8
@@ -453,9 +454,11 @@ def check_moe_layer_status(device: torch.device | None = None, stream: int | Non
 
 
 def lm_head_accept(h: torch.Tensor, lm_head: torch.Tensor, ids: torch.Tensor | None = None,
-                   want_logits: bool = True):
-    """(logits bf16 [T, V] | None, pred int64 [T], result int64 [2] = (n_accept, bonus_row))."""
-    dev = require_cuda(h, lm_head, ids)
+                   want_logits: bool = True, pred: torch.Tensor | None = None):
+    """(logits bf16 [T, V] | None, pred int64 [T], result int64 [2] = (n_accept, bonus_row)).
+    pred, if given, is where the argmax goes (contiguous int64 [T], e.g. a
+    slice of the next call's id buffer)."""
+    dev = require_cuda(h, lm_head, ids, pred)
     h = h.to(torch.bfloat16).contiguous()
     n, d = h.shape
     vocab = lm_head.shape[0]
@@ -466,7 +469,10 @@ def lm_head_accept(h: torch.Tensor, lm_head: torch.Tensor, ids: torch.Tensor | N
         if ids.numel() != n:
             raise ValueError("ids must have one entry per hidden row")
     logits = torch.empty(n, vocab, dtype=torch.bfloat16, device=dev) if want_logits else None
-    pred = torch.empty(n, dtype=torch.int64, device=dev)
+    if pred is None:
+        pred = torch.empty(n, dtype=torch.int64, device=dev)
+    elif pred.dtype != torch.int64 or not pred.is_contiguous() or pred.numel() != n:
+        raise ValueError("pred must be a contiguous int64 tensor of one entry per hidden row")
     result = torch.empty(2, dtype=torch.int64, device=dev)
     nbytes = lib().hsmoe_lm_head_workspace_size(n, vocab)
     ws = _workspace(dev, "lm_head", nbytes)
@@ -507,6 +513,86 @@ def add_rms_norm(x: torch.Tensor, weight: torch.Tensor, add: torch.Tensor | None
     check(lib().hsmoe_add_rms_norm(ptr(x2), ptr(add), ptr(residual), ptr(w), x2.shape[0], d, eps, ptr(h), ptr(out),
                                    stream_ptr(dev)), "hsmoe_add_rms_norm")
     return (None if h is None else h.reshape(shape)), out.reshape(shape)
+
+
+def _bf16_row(t: torch.Tensor, d: int, what: str) -> torch.Tensor:
+    t = t.to(torch.bfloat16).reshape(-1).contiguous()
+    if t.numel() != d:
+        raise ValueError(f"{what} must be one row of the hidden size")
+    return t
+
+
+def embed_add_rms_norm(ids: torch.Tensor, table: torch.Tensor, weight: torch.Tensor,
+                       residual: torch.Tensor | None = None, eps: float = 1e-6):
+    """The embedding lookup table[ids] followed by add_rms_norm(x, weight,
+    residual=residual, want_sum=True), in one launch -> (h, RMSNorm(h)), each
+    bf16 [*ids.shape, D]; an id outside [0, V) reads a row of zeros."""
+    dev = require_cuda(ids, table, weight, residual)
+    if table.dtype != torch.bfloat16 or table.dim() != 2 or not table.is_contiguous():
+        raise TypeError("the embedding table must be a contiguous bf16 [V, D] tensor")
+    vocab, d = table.shape
+    ids_flat = ids.reshape(-1).to(torch.int64).contiguous()
+    w = _bf16_row(weight, d, "norm weight")
+    res = None if residual is None else _bf16_row(residual, d, "residual")
+    rows = ids_flat.numel()
+    h = torch.empty(rows, d, dtype=torch.bfloat16, device=dev)
+    out = torch.empty_like(h)
+    check(lib().hsmoe_embed_add_rms_norm(ptr(ids_flat), rows, ptr(table), vocab, ptr(res), ptr(w), d, eps, ptr(h),
+                                         ptr(out), stream_ptr(dev)), "hsmoe_embed_add_rms_norm")
+    shape = tuple(ids.shape) + (d,)
+    return h.reshape(shape), out.reshape(shape)
+
+
+def mtp_input(tok: torch.Tensor, embed: torch.Tensor, h_prev: torch.Tensor, enorm: torch.Tensor,
+              hnorm: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor | None = None, eps: float = 1e-6):
+    """The MTP block's input for one draft token (tok: one int64 on the device):
+    h = RMSNorm(h_prev) * hnorm + RMSNorm(embed[tok]) * enorm (+ residual), as
+    bf16 adds -> (h [1, D], RMSNorm(h) * weight [1, D]), in one launch."""
+    dev = require_cuda(tok, embed, h_prev, enorm, hnorm, weight, residual)
+    if embed.dtype != torch.bfloat16 or embed.dim() != 2 or not embed.is_contiguous():
+        raise TypeError("the embedding table must be a contiguous bf16 [V, D] tensor")
+    vocab, d = embed.shape
+    tok = tok.reshape(-1).to(torch.int64).contiguous()
+    if tok.numel() != 1:
+        raise ValueError("mtp_input takes one token")
+    hp = _bf16_row(h_prev, d, "h_prev")
+    en, hn, w = (_bf16_row(t, d, "norm weight") for t in (enorm, hnorm, weight))
+    res = None if residual is None else _bf16_row(residual, d, "residual")
+    h = torch.empty(1, d, dtype=torch.bfloat16, device=dev)
+    out = torch.empty_like(h)
+    check(lib().hsmoe_mtp_input(ptr(tok), ptr(embed), vocab, ptr(hp), ptr(en), ptr(hn), ptr(res), ptr(w), d, eps,
+                                ptr(h), ptr(out), stream_ptr(dev)), "hsmoe_mtp_input")
+    return h, out
+
+
+def decode_step_record(tokens: torch.Tensor, pred: torch.Tensor | None = None, result: torch.Tensor | None = None,
+                       record: tuple | None = None, cur: torch.Tensor | None = None):
+    """A greedy step's emission from the verify's outputs, in one launch.
+    tokens int64 [1 + n] = [a, drafts]; pred int64 [1 + n] and result int64 [2]
+    (n_accept, bonus_row) of lm_head_accept (unused when n == 0).  -> (row
+    [n + 2] (or [1]), count, next, n_accept) device int64 tensors.  record =
+    (rows [cap, width], counts [cap], n_accepts [cap], k []) also writes row
+    k and advances k on the device; cur (one int64) receives next."""
+    dev = require_cuda(tokens, pred, result, cur)
+    tokens = tokens.reshape(-1)
+    n = tokens.numel() - 1
+    for t in (tokens, pred, result, cur) + (tuple(record) if record else ()):
+        if t is not None and (t.dtype != torch.int64 or not t.is_contiguous()):
+            raise TypeError("decode_step_record takes contiguous int64 tensors")
+    width = n + 2 if n > 0 else 1
+    outs = torch.empty(width + 3, dtype=torch.int64, device=dev)
+    rows = counts = naccs = k = None
+    cap = 0
+    if record is not None:
+        rows, counts, naccs, k = record
+        cap = rows.shape[0]
+        if rows.shape[1] != width or counts.numel() < cap or naccs.numel() < cap or k.numel() != 1:
+            raise ValueError("record buffers do not match the step's row width and capacity")
+    check(lib().hsmoe_decode_step_record(ptr(tokens), n, ptr(pred), ptr(result), ptr(outs),
+                                         outs.data_ptr() + 8 * width, outs.data_ptr() + 8 * (width + 1),
+                                         outs.data_ptr() + 8 * (width + 2), ptr(rows), ptr(counts), ptr(naccs),
+                                         ptr(k), cap, ptr(cur), stream_ptr(dev)), "hsmoe_decode_step_record")
+    return outs[:width], outs[width], outs[width + 1], outs[width + 2]
 
 
 def xor_checksum(data: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:

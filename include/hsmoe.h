@@ -339,6 +339,47 @@ int hsmoe_rms_norm(const void* x_dev, const void* w_dev, int64_t rows, int64_t d
 int hsmoe_add_rms_norm(const void* x_dev, const void* add_dev, const void* res_dev, const void* w_dev, int64_t rows,
                        int64_t d, float eps, void* h_out_dev, void* out_dev, hsmoe_stream_t stream);
 
+/* The first layer's input of a forward: the token embedding lookup
+ * (engine.py:2475 and 2814, self.embed[ids].to(bfloat16)) followed by hsmoe_add_rms_norm with
+ * no add: row r of x is row ids[r] of table [vocab, d] (an id outside
+ * [0, vocab) reads zeros), h = bf16(x + res) when res is given,
+ * h_out[r] = h, out[r] = RMSNorm(h).  Same arithmetic and order as the lookup
+ * followed by hsmoe_add_rms_norm, bit for bit. */
+int hsmoe_embed_add_rms_norm(const int64_t* ids_dev, int64_t rows, const void* table_dev, int64_t vocab,
+                             const void* res_dev, const void* w_dev, int64_t d, float eps, void* h_out_dev,
+                             void* out_dev, hsmoe_stream_t stream);
+
+/* The MTP block's input for one draft token (the data flow of the reference's
+ * draft step, engine.py:2251-2339, without its attention and projections):
+ *   e = RMSNorm(embed[tok[0]]) * enorm_w;  g = RMSNorm(h_prev) * hnorm_w;
+ *   h = bf16(g + e);  if res: h = bf16(h + res);
+ *   h_out = h;  out = RMSNorm(h) * w
+ * Each RMSNorm and add as hsmoe_add_rms_norm; bit-identical to the lookup,
+ * two norms, the add and the add + norm it replaces.  tok: one int64 on the
+ * device (read there: no host synchronisation); rows bf16 [d], d % 8 == 0,
+ * d <= 8192, 16-byte aligned. */
+int hsmoe_mtp_input(const int64_t* tok_dev, const void* embed_dev, int64_t vocab, const void* h_prev_dev,
+                    const void* enorm_w_dev, const void* hnorm_w_dev, const void* res_dev, const void* w_dev,
+                    int64_t d, float eps, void* h_out_dev, void* out_dev, hsmoe_stream_t stream);
+
+/* One greedy decode step's emission (engine.py:2862-2922 at temperature 0),
+ * from the verify's device outputs, with no host synchronisation:
+ * tokens = [a, d_0 .. d_{n-1}] (the verify's input ids, n = n_draft <= 15),
+ * pred = the verify's argmax per row, result = {n_accept, bonus_row} as
+ * hsmoe_lm_head_accept writes them (both unused when n_draft == 0).
+ *   row   = [a, d_0 .. d_{n-1}, pred[bonus_row]]   ([a] without drafts)
+ *   count = 1 + (n_accept > 0) * (n_accept + 1)    tokens emitted
+ *   next  = pred[bonus_row] if n_accept > 0 else a
+ * Each output pointer may be NULL.  With rows (then counts, n_accepts, k and
+ * capacity >= 1 too): row k of rows [capacity][width] (width n + 2, or 1),
+ * counts[k] and n_accepts[k] are written for k = *k in [0, capacity), then
+ * *k += 1; *cur = next (if cur).  One single-thread launch. */
+int hsmoe_decode_step_record(const int64_t* tokens_dev, int64_t n_draft, const int64_t* pred_dev,
+                             const int64_t* result_dev, int64_t* row_out_dev, int64_t* count_out_dev,
+                             int64_t* next_out_dev, int64_t* n_accept_out_dev, int64_t* rows_dev,
+                             int64_t* counts_dev, int64_t* n_accepts_dev, int64_t* k_dev, int64_t capacity,
+                             int64_t* cur_dev, hsmoe_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * XOR checksum of a device buffer: out (16 bytes) = XOR of the buffer's
  * 16-byte words.  Verifies the HBM expert store (or any slice of it) against a

@@ -107,20 +107,21 @@ def test_verify_rows_equal_single_token_forwards(model):
 
 
 def test_fused_stack_equals_layer_loop(model, monkeypatch):
-    """The fused chain (each layer launch ending with the next layer's adds +
-    RMSNorm, one add + norm launch before the first layer) gives the values of
-    the plain layer loop, bit for bit."""
+    """The fused chain (the embedding lookup in the first add + norm launch,
+    each layer launch ending with the next layer's adds + RMSNorm) gives the
+    values of the plain layer loop, bit for bit."""
     eng, _ = model
     ids = torch.tensor([[9, 400, 1000]], dtype=torch.int64, device=eng.device)
     h = eng._embed(ids)
     for l in range(NL):
         h, _ = eng._forward_layer(h, eng._get_layer_weights(l), l, ids)
     hf = eng._final_hidden(h)
-    n_norm = []
-    inner = ops.add_rms_norm
-    monkeypatch.setattr(ops, "add_rms_norm", lambda *a, **kw: n_norm.append(1) or inner(*a, **kw))
+    calls = []
+    for name in ("add_rms_norm", "embed_add_rms_norm"):
+        inner = getattr(ops, name)
+        monkeypatch.setattr(ops, name, lambda *a, _n=name, _f=inner, **kw: calls.append(_n) or _f(*a, **kw))
     h2, hf2 = eng._forward_stack(ids)
-    assert len(n_norm) == 1  # the norm tails did the rest
+    assert calls == ["embed_add_rms_norm"]  # the norm tails did the rest
     assert torch.equal(h, h2) and torch.equal(hf, hf2)
 
 
