@@ -66,7 +66,7 @@ constexpr unsigned kSpinLimit = 1u << 16;
 static_assert(kMaxExperts == kThreads && kMaxExperts == 4 * 64, "plan build: one expert per thread, four per lane");
 
 // Control words (unsigned) at the start of the workspace.  Every handoff
-// between items is a tagged word (tag << 32 | fp32 bits, see launch_tag),
+// between items is a tagged word (tag << 32 | fp32 bits, see read_launch_tag),
 // polled until it carries this launch's tag; the only counter counts the
 // workgroups that finished, so that the last one can advance the epoch.
 constexpr int kCtlEpoch = 0;     // tag of the previous launch (0: none yet)
@@ -139,7 +139,10 @@ struct LayerParams {
 
 // This launch's tag: the previous launch's plus one (never 0).  The epoch word
 // changes only after every workgroup of the launch has finished its items.
-__device__ __forceinline__ unsigned launch_tag(const unsigned* ctl) {
+// Read once per workgroup, at its start, into the workgroup's LDS (g_sh.tag):
+// every wave of every item reading the one epoch word with agent-scope loads
+// queued thousands of same-address reads at the coherence point.
+__device__ __forceinline__ unsigned read_launch_tag(const unsigned* ctl) {
   const unsigned ep = load_agent(ctl + kCtlEpoch);
   return ep == 0xffffffffu ? 1u : ep + 1u;
 }
@@ -186,6 +189,7 @@ struct Shared {
   int eid[kMaxSlots];            // slot plan: expert id of routed slot s
   float wt[kMaxSlots][kMaxTok];  // slot plan: weight of routed slot s for token t
   float wt_item[kMaxTok];
+  unsigned tag;  // this launch's tag (read_launch_tag, once per workgroup)
   int flag;
   int n_routed;
   int have_plan;
@@ -222,7 +226,7 @@ __device__ __forceinline__ void build_plan_scores(const LayerParams& p, Shared& 
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       w[j][q] = (cur & (1u << (4 * j + q))) ? load_agent(copy + (wave + kWaves * j) * p.n_exp + lane + 64 * q) : 0ull;
-  const unsigned tag = launch_tag(p.ctl);
+  const unsigned tag = sh.tag;
   bool seen = false;
   for (unsigned it = 0; it < kSpinLimit; ++it) {
 #pragma unroll
@@ -461,7 +465,7 @@ __device__ __forceinline__ int router_item(uint64_t kernarg, int q_arg, int stat
     const int c = threadIdx.x + kThreads * j;
     wv[j] = c < nch ? ldg<uint4>(wrow + c) : make_uint4(0, 0, 0, 0);
   }
-  const unsigned tag = launch_tag(p.ctl);
+  const unsigned tag = g_sh.tag;
   const float bias_v = p.bias && threadIdx.x < p.m ? ldg<float>(p.bias + e) : 0.0f;
   ensure_x(p, state);
 #pragma unroll 1
@@ -503,7 +507,7 @@ __device__ __noinline__ int gate_up_item(uint64_t kernarg, int q_arg, int state_
   const int s = qq / gu_per_slot;
   const int r0 = (qq % gu_per_slot) * kGuRows;
   if (s >= sh.n_routed) return state;
-  const unsigned tag = launch_tag(p.ctl);
+  const unsigned tag = g_sh.tag;
   if (threadIdx.x < p.m) sh.wt_item[threadIdx.x] = sh.wt[s][threadIdx.x];
   const uint64_t* ent = sh.ent[s];
   ensure_x(p, state);
@@ -553,7 +557,7 @@ __device__ __noinline__ int shared_half_item(uint64_t kernarg, int q_arg, int st
   // that they run on one XCD when workgroups are dealt to the 8 XCDs in turn
   const int k = q - p.sgu0, blk = k >> 4, span = min(8, p.i / kGuRows - 8 * blk);
   const int mat = (k & 15) >= span, r0 = (8 * blk + (k & 15) - mat * span) * kGuRows;
-  const unsigned tag = launch_tag(p.ctl);
+  const unsigned tag = g_sh.tag;
   const uint64_t* ent = sh.ent[p.S];
   ensure_x(p, state);
   const int per = (p.d / 128) / kWaves;
@@ -605,7 +609,7 @@ __device__ __noinline__ int gate_up_run(uint64_t kernarg, int q_arg, int state_a
   const int G = (int)gridDim.x, gu_per_slot = p.i / kGuRows;
   const int per = (p.d / 128) / kWaves, nb = per / kB, st0 = wave * per;
   ensure_x(p, state);
-  const unsigned tag = launch_tag(p.ctl);
+  const unsigned tag = g_sh.tag;
   int s = (q - p.gu0) / gu_per_slot, r0 = ((q - p.gu0) % gu_per_slot) * kGuRows;
   Mat w1 = make_mat<F>(sh.ent[s][0], sh.ent[s][1], p.i, p.d), w3 = make_mat<F>(sh.ent[s][2], sh.ent[s][3], p.i, p.d);
   Batch<F, kB> b1, b3;
@@ -736,7 +740,7 @@ __device__ __noinline__ int down_item(uint64_t kernarg, int q_arg, int state_arg
   down_slot_of(p, q, is_shared_q, s, g, h);
   constexpr bool is_shared = kShared;
   if (!is_shared && s >= sh.n_routed) return state;
-  const unsigned tag = launch_tag(p.ctl);  // (issued before the weight loads)
+  const unsigned tag = g_sh.tag;
   const uint64_t* ent = sh.ent[s];
   // shared: waves 0 and 2 (1 and 3) take rows r0 .. r0 + 15 over the first
   // (second) step range
@@ -867,7 +871,7 @@ __device__ __noinline__ void down_finish(uint64_t kernarg, int q_arg) {
   int last = n_routed > 0 ? down_index(p, n_routed - 1, g) : -1;
   if (p.shared && p.sd0 + 2 * g + 1 > last) last = p.sd0 + 2 * g + 1;
   if (q != last) return;
-  const unsigned tag = launch_tag(p.ctl);
+  const unsigned tag = g_sh.tag;
   const int m = p.m;
   const int64_t stride = (int64_t)m * p.d;  // between slots
   for (int c0 = 0; c0 < kDownRows * m; c0 += kThreads) {
@@ -911,7 +915,7 @@ __device__ __noinline__ void down_finish(uint64_t kernarg, int q_arg) {
 __device__ __noinline__ void tail_item(uint64_t kernarg, int t_arg) {
   const int t = __builtin_amdgcn_readfirstlane(t_arg);
   const LayerParams p = params(kernarg);
-  const unsigned tag = launch_tag(p.ctl);
+  const unsigned tag = g_sh.tag;
   const bool zero = g_sh.n_routed == 0 && !p.shared;
   const int tid = (int)threadIdx.x;
   const int chunks = p.d / 8;  // d <= 8192: at most 4 chunks per thread
@@ -988,7 +992,10 @@ __device__ __noinline__ void tail_item(uint64_t kernarg, int t_arg) {
 
 __global__ void __launch_bounds__(kThreads, 2) moe_layer_kernel(LayerParams p) {
   int state = 0;  // 1 while the LDS tile holds x, 2 + s while routed slot s's activations
-  if (threadIdx.x == 0) g_sh.have_plan = 0;
+  if (threadIdx.x == 0) {
+    g_sh.have_plan = 0;
+    g_sh.tag = read_launch_tag(p.ctl);  // visible to every wave after the first item's barrier
+  }
   if (p.shared && threadIdx.x < 6) g_sh.ent[p.S][threadIdx.x] = ldg<uint64_t>(p.shared + threadIdx.x);
   const uint64_t kernarg = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();  // &p
   const int n_main = p.n_main, n_router = p.n_router;
@@ -1047,7 +1054,7 @@ __global__ void __launch_bounds__(kThreads, 2) moe_layer_kernel(LayerParams p) {
   if (threadIdx.x == 0) g_sh.last = add_agent(p.ctl + kCtlDone, 1u) == gridDim.x - 1;
   __syncthreads();
   if (!g_sh.last) return;
-  const unsigned tag = launch_tag(p.ctl);
+  const unsigned tag = g_sh.tag;
   if (tag >= kRearmTag) {
     const uint4 zero = {0u, 0u, 0u, 0u};
     for (int64_t k = threadIdx.x; k < p.wipe_n; k += kThreads) p.wipe[k] = zero;

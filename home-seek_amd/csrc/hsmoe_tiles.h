@@ -156,14 +156,6 @@ constexpr int down_batch() {
   return (F == kFp4E8M0 || F == kFp4F32 || kDeep) ? 2 * gate_up_batch<F>() : gate_up_batch<F>();
 }
 
-// Largest batch size <= kMax (a power of two) that divides n.
-template <int kMax>
-__device__ __forceinline__ int batch_for(int n) {
-  int b = kMax;
-  while (b > 1 && n % b != 0) b >>= 1;
-  return b;
-}
-
 // Format of the slot whose table entry is `ent`.
 __device__ __forceinline__ int slot_format(int routed_scale_fmt, const uint64_t* ent, bool is_shared) {
   if (is_shared) return ent[1] ? kFp8Block : kBf16;
@@ -221,10 +213,7 @@ template <int F>
 __device__ __forceinline__ void gate_up_any(const uint64_t* ent, const uint16_t* xs, int m, int d, int i, int r0,
                                             int st0, int st1, f32x4& ag, f32x4& au) {
   constexpr int kMax = gate_up_batch<F>();
-  const int b = batch_for<kMax>(st1 - st0);
-  if (b == kMax) gate_up_rows<F, kMax>(ent, xs, m, d, i, r0, st0, st1, ag, au);
-  else if (kMax > 4 && b == 4) gate_up_rows<F, (kMax > 4 ? 4 : 1)>(ent, xs, m, d, i, r0, st0, st1, ag, au);
-  else if (kMax > 2 && b == 2) gate_up_rows<F, (kMax > 2 ? 2 : 1)>(ent, xs, m, d, i, r0, st0, st1, ag, au);
+  if ((st1 - st0) % kMax == 0) gate_up_rows<F, kMax>(ent, xs, m, d, i, r0, st0, st1, ag, au);
   else gate_up_rows<F, 1>(ent, xs, m, d, i, r0, st0, st1, ag, au);
 }
 
@@ -257,17 +246,15 @@ __device__ __forceinline__ void gate_or_up_rows(uint64_t w, uint64_t sc, const u
   }
 }
 
-// gate_or_up_rows with the largest batch (at most twice the gate/up batch:
-// one matrix instead of two) that divides the steps.
+// gate_or_up_rows in batches of twice the gate/up batch (one matrix instead
+// of two) when that divides the steps, else one step at a time (the *_any
+// helpers instantiate only these two sizes: every further size is code that
+// the decode shapes never run, fetched into the instruction cache nonetheless).
 template <int F>
 __device__ __forceinline__ void gate_or_up_any(uint64_t w, uint64_t sc, const uint16_t* xs, int m, int d, int i,
                                                int r0, int st0, int st1, f32x4& acc) {
   constexpr int kMax = 2 * gate_up_batch<F>();
-  const int b = batch_for<kMax>(st1 - st0);
-  if (b == kMax) gate_or_up_rows<F, kMax>(w, sc, xs, m, d, i, r0, st0, st1, acc);
-  else if (kMax > 8 && b == 8) gate_or_up_rows<F, (kMax > 8 ? 8 : 1)>(w, sc, xs, m, d, i, r0, st0, st1, acc);
-  else if (kMax > 4 && b == 4) gate_or_up_rows<F, (kMax > 4 ? 4 : 1)>(w, sc, xs, m, d, i, r0, st0, st1, acc);
-  else if (kMax > 2 && b == 2) gate_or_up_rows<F, (kMax > 2 ? 2 : 1)>(w, sc, xs, m, d, i, r0, st0, st1, acc);
+  if ((st1 - st0) % kMax == 0) gate_or_up_rows<F, kMax>(w, sc, xs, m, d, i, r0, st0, st1, acc);
   else gate_or_up_rows<F, 1>(w, sc, xs, m, d, i, r0, st0, st1, acc);
 }
 
@@ -311,16 +298,13 @@ __device__ __forceinline__ void down_rows(const uint64_t* ent, const uint16_t* a
   }
 }
 
-// kCap: the largest batch instantiated (steps loaded per round).
+// Batches of min(down_batch, kCap) steps when that divides the steps, else one
+// step at a time.
 template <int F, bool kDeep, int kCap = 64, typename Ready>
 __device__ __forceinline__ void down_any(const uint64_t* ent, const uint16_t* as, int m, int i, int d, int r0,
                                          int st0, int st1, f32x4& acc, Ready&& ready) {
   constexpr int kMax = down_batch<F, kDeep>() < kCap ? down_batch<F, kDeep>() : kCap;
-  const int b = batch_for<kMax>(st1 - st0);
-  if (b == kMax) down_rows<F, kMax>(ent, as, m, i, d, r0, st0, st1, acc, ready);
-  else if (kMax > 8 && b == 8) down_rows<F, (kMax > 8 ? 8 : 1)>(ent, as, m, i, d, r0, st0, st1, acc, ready);
-  else if (kMax > 4 && b == 4) down_rows<F, (kMax > 4 ? 4 : 1)>(ent, as, m, i, d, r0, st0, st1, acc, ready);
-  else if (kMax > 2 && b == 2) down_rows<F, (kMax > 2 ? 2 : 1)>(ent, as, m, i, d, r0, st0, st1, acc, ready);
+  if ((st1 - st0) % kMax == 0) down_rows<F, kMax>(ent, as, m, i, d, r0, st0, st1, acc, ready);
   else down_rows<F, 1>(ent, as, m, i, d, r0, st0, st1, acc, ready);
 }
 
