@@ -356,12 +356,53 @@ __device__ __forceinline__ void pipeline(const uint64_t* ent, int w_slot, int n_
 }
 
 // ---------------------------------------------------------------- gate / up
+// The E8M0 scale bytes lane (r, g) needs for steps [s0, s0 + kSteps) of
+// weight row `row` (k columns): byte j of c[q] is the group-g scale of step
+// s0 + 4q + j.  A K-chunk uses two steps' bytes; reading them per K-chunk
+// touched each row's 128-byte scale line sixteen times, far enough apart in
+// time that the weight stream had evicted it from L2 in between (measured:
+// ~0.6 GB of the gate/up fetch of the M=512 prefill against 0.13 GB of
+// scales).  fill() reads the row's kSteps steps of scales once (lane g: steps
+// s0 + 4g .. +3, 16 bytes) and deals each step's word to the row's four lanes
+// (ds_bpermute from lanes r + 16q); consume() advances past a K-chunk.
+struct ScaleCache {
+  static constexpr int kSteps = 16;  // 8 K-chunks
+  uint32_t c[4];
+  __device__ __forceinline__ void fill(const BufRsrc& s, int row, int k, int s0, int g) {
+    const int r = (threadIdx.x & 63) & 15;
+    const uint4 u = bload128(s, (uint32_t)row * (uint32_t)(k / 32) + (uint32_t)(s0 + 4 * g) * 4);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c[q] = 0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t v = (uint32_t)__builtin_amdgcn_ds_bpermute((r + 16 * q) * 4, (int)w[j]);
+        c[q] |= ((v >> (8 * g)) & 0xffu) << (8 * j);
+      }
+  }
+  // scale byte of step b of K-chunk kc (two steps per K-chunk)
+  __device__ __forceinline__ uint32_t byte(int kc, int b) const { return (c[0] >> (8 * (2 * (kc & 1) + b))) & 0xffu; }
+  __device__ __forceinline__ void consume(int kc) {
+    if (kc & 1) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q) c[q] = c[q + 1];
+      c[3] = 0u;
+    }
+  }
+};
+
 // Wave rows r0 .. r0+16*kGuRT-1 of W1 and W3 against the chunk's tokens; lane
 // (r, g) ends holding rows r0 + 16 rt + 4g + q of token tile*16 + r.
+// F = kFp4E8M0Split: E8M0 scales through a ScaleCache per matrix (the same
+// decoded weights as kFp4E8M0).
 template <int F, int kC, int kBufs>
 __device__ void gate_up_chunk(const PrefillParams& p, const Chunk& ch, int r0, uint16_t* xs, const int* s_tok) {
   using W = WBuf<F, 2, kGuRT>;
   constexpr int kTiles = kC / 16;
+  constexpr bool kSplit = F == kFp4E8M0Split;
+  static_assert(!kSplit || (kGuRT == 1 && W::kSteps == 2), "scale cache: one row tile, two steps per K-chunk");
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int ntile = (ch.n + 15) / 16;
   f32x4 ag[kGuRT][kTiles], au[kGuRT][kTiles];
@@ -369,15 +410,40 @@ __device__ void gate_up_chunk(const PrefillParams& p, const Chunk& ch, int r0, u
   for (int rt = 0; rt < kGuRT; ++rt)
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) ag[rt][t] = au[rt][t] = f32x4{0, 0, 0, 0};
+  ScaleCache s1, s3;
+  const BufRsrc sr1 = make_mat<F>(ch.ent[0], ch.ent[1], p.i, p.d).s, sr3 = make_mat<F>(ch.ent[2], ch.ent[3], p.i, p.d).s;
+  if constexpr (kSplit) {
+    s1.fill(sr1, r0 + r, p.d, 0, g);
+    s3.fill(sr3, r0 + r, p.d, 0, g);
+  }
+  int kc = 0;
   auto src = [&](int, int tt) { return p.x + (int64_t)s_tok[tt] * p.d; };
   pipeline<F, 2, kGuRT, 1, kC, kBufs>(ch.ent, 0, p.i, r0 + r, p.d, g, ch.n, xs, src, [&](const W& w) {
+    if constexpr (kSplit) {
+      if (kc > 0 && (kc & (ScaleCache::kSteps / 2 - 1)) == 0) {  // the next kSteps steps' scales
+        s1.fill(sr1, r0 + r, p.d, 2 * kc, g);
+        s3.fill(sr3, r0 + r, p.d, 2 * kc, g);
+      }
+    }
 #pragma unroll
     for (int b = 0; b < W::kSteps; ++b) {
+      uint32_t e1 = 0, e3 = 0;
+      if constexpr (kSplit) {
+        e1 = s1.byte(kc, b);
+        e3 = s3.byte(kc, b);
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
 #pragma unroll
         for (int rt = 0; rt < kGuRT; ++rt) {
-          const bf16x8 f1 = w.b[0][rt].frag(b, j, g), f3 = w.b[1][rt].frag(b, j, g);
+          bf16x8 f1, f3;
+          if constexpr (kSplit) {
+            f1 = w.b[0][rt].frag_e(b, j, e1);
+            f3 = w.b[1][rt].frag_e(b, j, e3);
+          } else {
+            f1 = w.b[0][rt].frag(b, j, g);
+            f3 = w.b[1][rt].frag(b, j, g);
+          }
 #pragma unroll
           for (int tile = 0; tile < kTiles; ++tile) {
             if (tile >= ntile) break;
@@ -388,6 +454,11 @@ __device__ void gate_up_chunk(const PrefillParams& p, const Chunk& ch, int r0, u
         }
       }
     }
+    if constexpr (kSplit) {
+      s1.consume(kc);
+      s3.consume(kc);
+    }
+    ++kc;
   });
 #pragma unroll
   for (int tile = 0; tile < kTiles; ++tile) {
@@ -424,8 +495,10 @@ prefill_gate_up_kernel(PrefillParams p) {
   if (threadIdx.x < kBigChunk) s_tok[threadIdx.x] = threadIdx.x < ch.n ? p.pair_tok[ch.p0 + threadIdx.x] : 0;
   __syncthreads();
   const int r0 = (blockIdx.x % nrb) * kGuRows + 16 * kGuRT * (threadIdx.x >> 6);
+  // routed E8M0 chunks read their scales through a per-lane cache (same weights)
+  constexpr int FG = F == kFp4E8M0 ? kFp4E8M0Split : F;
   if (!kShared && ch.n > kChunk && ch.ent[1]) {  // a big expert's chunk (the shared expert's hold at most kChunk)
-    gate_up_chunk<F, kBigChunk, 1>(p, ch, r0, xs, s_tok);
+    gate_up_chunk<FG, kBigChunk, 1>(p, ch, r0, xs, s_tok);
   } else if (ch.n > kChunk) {  // bf16 weights: the chunk as two kChunk halves (registers)
     for (int h0 = 0; h0 < ch.n; h0 += kChunk) {
       Chunk sub = ch;
@@ -434,7 +507,7 @@ prefill_gate_up_kernel(PrefillParams p) {
       gate_up_chunk<kBf16, kChunk, 3>(p, sub, r0, xs, s_tok + h0);
     }
   } else if (ch.ent[1]) {
-    gate_up_chunk<F, kChunk, 3>(p, ch, r0, xs, s_tok);
+    gate_up_chunk<FG, kChunk, 3>(p, ch, r0, xs, s_tok);
   } else {
     gate_up_chunk<kBf16, kChunk, 3>(p, ch, r0, xs, s_tok);
   }

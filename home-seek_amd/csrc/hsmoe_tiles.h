@@ -16,7 +16,9 @@
 
 namespace hsmoe {
 
-enum Fmt : int { kFp4E8M0 = 0, kFp4F32 = 1, kFp8Block = 2, kBf16 = 3 };
+enum Fmt : int { kFp4E8M0 = 0, kFp4F32 = 1, kFp8Block = 2, kBf16 = 3, kFp4E8M0Split = 4 };
+// kFp4E8M0Split: FP4 with E8M0 scales whose bytes the caller reads itself
+// (batches hold the weights only; the matrix is that of kFp4E8M0).
 
 // One weight matrix of format F ([rows][cols], row-major) and its scales, as
 // buffer resources of their exact sizes: every load of a batch is an
@@ -29,7 +31,7 @@ template <int F>
 __device__ __forceinline__ Mat make_mat(uint64_t w, uint64_t sc, int rows, int cols) {
   const uint32_t n = (uint32_t)rows * (uint32_t)cols;
   Mat m;
-  if constexpr (F == kFp4E8M0) {
+  if constexpr (F == kFp4E8M0 || F == kFp4E8M0Split) {
     m.w = make_buf(w, n / 2);
     m.s = make_buf(sc, n / 32);
   } else if constexpr (F == kFp4F32) {
@@ -81,6 +83,22 @@ struct Batch<kFp4E8M0, kB> {
     } else {
       e = (sw[b] >> (8 * g)) & 0xffu;
     }
+    return fp4x8_to_bf16_e8m0(dw, e8m0_as_f32(e));
+  }
+};
+
+template <int kB>
+struct Batch<kFp4E8M0Split, kB> {
+  uint4 a[kB];
+  __device__ __forceinline__ void load(const Mat& m, int row, int k, int st, int g) {
+    const uint32_t wo = (uint32_t)row * (uint32_t)(k / 2) + st * 64 + g * 16;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) a[b] = bload128(m.w, wo + b * 64);
+  }
+  // the weights of MFMA j of step b, decoded with scale exponent byte e
+  __device__ __forceinline__ bf16x8 frag_e(int b, int j, uint32_t e) const {
+    const uint4& q = a[b];
+    const uint32_t dw = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
     return fp4x8_to_bf16_e8m0(dw, e8m0_as_f32(e));
   }
 };
