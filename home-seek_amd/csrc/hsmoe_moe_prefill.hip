@@ -514,17 +514,33 @@ prefill_gate_up_kernel(PrefillParams p) {
 }
 
 // ---------------------------------------------------------------- down
+// F = kFp4E8M0Split: W2's E8M0 scales through a ScaleCache per row tile.
 template <int F>
 __device__ void down_chunk(const PrefillParams& p, const Chunk& ch, int r0, uint16_t* as) {
   using W = WBuf<F, 1, kDnRT>;
+  constexpr bool kSplit = F == kFp4E8M0Split;
+  static_assert(!kSplit || W::kSteps == 2, "scale cache: two steps per K-chunk");
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int ntile = (ch.n + 15) / 16;
   const uint16_t* ls = as + kChunk * (kCols + kPad);
   f32x4 acc[kDnRT][2];
 #pragma unroll
   for (int rt = 0; rt < kDnRT; ++rt) acc[rt][0] = acc[rt][1] = f32x4{0, 0, 0, 0};
+  ScaleCache sc[kDnRT];
+  const BufRsrc sr = make_mat<F>(ch.ent[4], ch.ent[5], p.d, p.i).s;
+  if constexpr (kSplit) {
+#pragma unroll
+    for (int rt = 0; rt < kDnRT; ++rt) sc[rt].fill(sr, r0 + r + 16 * rt, p.i, 0, g);
+  }
+  int kc = 0;
   auto src = [&](int pl, int tt) { return (pl ? p.act_lo : p.act_hi) + (int64_t)(ch.p0 + tt) * p.i; };
   pipeline<F, 1, kDnRT, 2, kChunk, 3>(ch.ent, 4, p.d, r0 + r, p.i, g, ch.n, as, src, [&](const W& w) {
+    if constexpr (kSplit) {
+      if (kc > 0 && (kc & (ScaleCache::kSteps / 2 - 1)) == 0) {  // the next kSteps steps' scales
+#pragma unroll
+        for (int rt = 0; rt < kDnRT; ++rt) sc[rt].fill(sr, r0 + r + 16 * rt, p.i, 2 * kc, g);
+      }
+    }
 #pragma unroll
     for (int b = 0; b < W::kSteps; ++b) {
 #pragma unroll
@@ -535,13 +551,20 @@ __device__ void down_chunk(const PrefillParams& p, const Chunk& ch, int r0, uint
           const bf16x8 hf = tile_frag(as, kCols, tile, r, g, b, j), lf = tile_frag(ls, kCols, tile, r, g, b, j);
 #pragma unroll
           for (int rt = 0; rt < kDnRT; ++rt) {
-            const bf16x8 wf = w.b[0][rt].frag(b, j, g);
+            bf16x8 wf;
+            if constexpr (kSplit) wf = w.b[0][rt].frag_e(b, j, sc[rt].byte(kc, b));
+            else wf = w.b[0][rt].frag(b, j, g);
             acc[rt][tile] = mfma16x16x32(wf, hf, acc[rt][tile]);
             acc[rt][tile] = mfma16x16x32(wf, lf, acc[rt][tile]);
           }
         }
       }
     }
+    if constexpr (kSplit) {
+#pragma unroll
+      for (int rt = 0; rt < kDnRT; ++rt) sc[rt].consume(kc);
+    }
+    ++kc;
   });
 #pragma unroll
   for (int tile = 0; tile < 2; ++tile) {
@@ -563,7 +586,7 @@ prefill_down_kernel(PrefillParams p) {
   Chunk ch;
   if (!load_chunk<kShared, true>(p, blockIdx.x / nrb, ch)) return;
   const int r0 = (blockIdx.x % nrb) * kDnRows + 16 * kDnRT * (threadIdx.x >> 6);
-  if (ch.ent[1]) down_chunk<F>(p, ch, r0, as);
+  if (ch.ent[1]) down_chunk<F == kFp4E8M0 ? kFp4E8M0Split : F>(p, ch, r0, as);  // routed E8M0: cached scales
   else down_chunk<kBf16>(p, ch, r0, as);
 }
 
