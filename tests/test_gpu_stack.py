@@ -347,3 +347,38 @@ def test_checkpoint_round_trip_through_the_loader(model, tmp_path):
         b, _ = eng2._forward_ffn(hn, lw2, l, ids)
         assert torch.equal(a, b), l
     assert ops.moe_layer_status(eng.device) == 0
+
+
+def test_layer_status_word_fails_the_verify_and_the_decoder(model):
+    """A nonzero sticky status word in a layer workspace (written here from the
+    host: no kernel gives up) makes _mtp_verify_batched and
+    GreedyDecoder.result() raise, leaves _global_pos where it was, and is
+    reported once (cleared after the raise)."""
+    from home_seek_amd import _lib
+    from home_seek_amd.engine import GreedyDecoder
+    eng, _ = model
+    dev = eng.device
+    main = torch.tensor([[7]], dtype=torch.int64, device=dev)
+    drafts = torch.tensor([[5, 6]], dtype=torch.int64, device=dev)
+    eng._mtp_verify_batched(drafts, main_pred_id=main)  # the layer workspaces exist after this
+    words = ops.moe_layer_status_words(dev)
+    assert words and ops.moe_layer_status(dev) == 0
+    pos = eng._global_pos
+    words[0].fill_(1 + 4612)
+    with pytest.raises(_lib.HsmoeError, match="gave up"):
+        eng._mtp_verify_batched(drafts, main_pred_id=main)
+    assert eng._global_pos == pos
+    assert ops.moe_layer_status(dev) == 0
+    n, logits = eng._mtp_verify_batched(drafts, main_pred_id=main)  # a clean verify works again
+    assert logits is not None and 0 <= n <= 2
+    dec = GreedyDecoder(eng, 2, graph=False)
+    dec.reset(11)
+    dec.run(1)
+    ops.moe_layer_status_words(dev)[0].fill_(1 + 4609)
+    with pytest.raises(_lib.HsmoeError, match="gave up"):
+        dec.result()
+    assert ops.moe_layer_status(dev) == 0
+    dec.reset(11)
+    dec.run(1)
+    tokens, accs = dec.result()
+    assert len(tokens) >= 1 and len(accs) == 1
