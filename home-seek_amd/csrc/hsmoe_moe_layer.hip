@@ -427,6 +427,35 @@ __device__ __noinline__ void plan_item(uint64_t kernarg) {
   if (blockIdx.x == gridDim.x - 1) write_routing(p, sh);  // read only after the launch
 }
 
+// plan_item for given routing when a gate/up item comes next and the LDS
+// tile does not hold x: it also copies x into the tile, by LDS-DMA loads
+// (global_load_lds_dwordx4: lane l of a wave writes 16 bytes at the wave's
+// base + 16 l, the tile's own layout) issued before the table entries and
+// the ids, so that x and the plan's inputs share one memory round trip and
+// no register holds x meanwhile.  The tile then holds x.
+__device__ __noinline__ void plan_x_item(uint64_t kernarg) {
+  const LayerParams p = params(kernarg);
+  Shared& sh = g_sh;
+  __syncthreads();  // the previous item's readers of the tile are done
+  const int n16 = p.m * p.d / 8, wave = threadIdx.x >> 6;
+  const uint4* src = reinterpret_cast<const uint4*>(p.x);
+  typedef __attribute__((address_space(3))) char LdsByte;
+  LdsByte* const tile = (LdsByte*)g_tile;
+  for (int c0 = 0; c0 < n16; c0 += kThreads) {
+    const int c = c0 + (int)threadIdx.x;
+    LdsByte* const dst = tile + 16 * (c0 + 64 * wave);  // wave-uniform base
+    if (c < n16) __builtin_amdgcn_global_load_lds((const void*)(src + c), (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+  }
+  uint64_t my_ent[6];
+#pragma unroll
+  for (int k = 0; k < 6; ++k)
+    my_ent[k] = (int)threadIdx.x < p.n_exp ? ldg<uint64_t>(p.table + (int64_t)threadIdx.x * 6 + k) : 0ull;
+  build_plan(p, sh, my_ent);
+  if (blockIdx.x == gridDim.x - 1) write_routing(p, sh);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-DMA loads have landed
+  __syncthreads();                // and every wave's
+}
+
 // Copies x into the LDS tile unless it is already there (state: 1 = x in LDS).
 __device__ __forceinline__ void ensure_x(const LayerParams& p, int& state) {
   if (state == 1) return;
@@ -999,6 +1028,10 @@ __global__ void __launch_bounds__(kThreads, 2) moe_layer_kernel(LayerParams p) {
   if (p.shared && threadIdx.x < 6) g_sh.ent[p.S][threadIdx.x] = ldg<uint64_t>(p.shared + threadIdx.x);
   const uint64_t kernarg = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();  // &p
   const int n_main = p.n_main, n_router = p.n_router;
+  // x comes with the slot plan only where the plan's inputs are in memory
+  // (given routing); with the router, x in the plan's round trip measured
+  // slower at M=3 (77.9 us against 77.6) and equal at M=1
+  const bool given = p.route_idx != nullptr;
   int q = blockIdx.x;
   for (; q < n_main; q += gridDim.x) {
     __syncthreads();  // the previous item's readers of the LDS scratch are done
@@ -1012,11 +1045,26 @@ __global__ void __launch_bounds__(kThreads, 2) moe_layer_kernel(LayerParams p) {
     }
     if (q >= p.sd0 && q < p.sd1) {  // shared down: the plan is needed only for its arrival
       state = down_item<true>(kernarg, q, state);
-      if (!g_sh.have_plan) plan_item(kernarg);
+      if (!g_sh.have_plan) {
+        const int qn = q + (int)gridDim.x;  // a gate/up item next: x comes with the plan
+        if (given && qn >= p.gu0 && qn < p.gu1 && qn < n_main) {
+          plan_x_item(kernarg);
+          state = 1;
+        } else {
+          plan_item(kernarg);
+        }
+      }
       down_finish(kernarg, q);
       continue;
     }
-    if (!g_sh.have_plan) plan_item(kernarg);  // routed items need the slot plan
+    if (!g_sh.have_plan) {  // routed items need the slot plan (given routing: a gate/up item x too)
+      if (given && state != 1 && q >= p.gu0 && q < p.gu1) {
+        plan_x_item(kernarg);
+        state = 1;
+      } else {
+        plan_item(kernarg);
+      }
+    }
     if (q >= p.gu0 && q < p.gu1) {
       const int s = (q - p.gu0) / (p.i / kGuRows);
       const int fmt = s < g_sh.n_routed ? slot_format(p.scale_fmt, g_sh.ent[s], false) : -1;
