@@ -90,7 +90,8 @@ __global__ void __launch_bounds__(kThreads) xor_fold_kernel(const uint4* __restr
 
 int grid_for(int64_t n16) {
   int cus = 256, dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
   const int64_t n_chunks = (n16 + kChunk - 1) / kChunk;
   int64_t g = 4 * (int64_t)cus;  // 4 workgroups (16 waves) per CU
   if (g > kMaxGrid) g = kMaxGrid;

@@ -336,7 +336,6 @@ __device__ __forceinline__ void finish_plan(const LayerParams& p, Shared& sh, co
 // slot being its weight for that id (a token's ids are distinct: at most
 // one), else 0 -- the union of _forward_legacy, fused_moe.py:466-476.
 __device__ __forceinline__ void build_plan(const LayerParams& p, Shared& sh, const uint64_t (&my_ent)[6]) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = p.m * p.top_k;
   if (p.route_idx) {
     // given routing: nothing to wait for (ids of tokens outside the table: -1)
@@ -391,9 +390,9 @@ __shared__ Shared g_sh;
 typedef const __attribute__((address_space(4))) LayerParams KernargParams;
 
 __device__ __forceinline__ LayerParams params(uint64_t kernarg) {
+#if defined(__HIP_DEVICE_COMPILE__)
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)kernarg);
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(kernarg >> 32));
-#if defined(__HIP_DEVICE_COMPILE__)
   return *(KernargParams*)(((uint64_t)hi << 32) | lo);
 #else
   return LayerParams{};  // host pass: never called
@@ -404,9 +403,9 @@ __device__ __forceinline__ LayerParams params(uint64_t kernarg) {
 // the compiler cannot hoist): held across down_finish's polls, the pointer
 // made that function save a callee-saved register to scratch.
 __device__ __forceinline__ uint64_t* fin_late(uint64_t kernarg) {
+#if defined(__HIP_DEVICE_COMPILE__)
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)kernarg);
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(kernarg >> 32));
-#if defined(__HIP_DEVICE_COMPILE__)
   return ((const volatile KernargParams*)(((uint64_t)hi << 32) | lo))->fin;
 #else
   return nullptr;

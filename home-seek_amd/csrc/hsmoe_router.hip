@@ -31,7 +31,7 @@ __global__ void __launch_bounds__(64 * kLogitWaves)
                   float* __restrict__ w_out) {
   extern __shared__ __align__(16) uint16_t xs[];  // [nt][d]
   __shared__ int s_last;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave = threadIdx.x >> 6;
   const int64_t e = (int64_t)blockIdx.x * kLogitWaves + wave;
   const int64_t t0 = (int64_t)blockIdx.y * kTok;
   const int nt = (int)((m - t0) < kTok ? (m - t0) : kTok);

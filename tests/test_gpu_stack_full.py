@@ -217,17 +217,17 @@ def test_full_size_decode_step_teacher_forced(eng):
                       np16(h), np16(hn)))
         return (h if want_sum else None), hn
 
-    def head(h, lm_head, ids=None, want_logits=True):
-        lg, pred, res = inner_head(h, lm_head, ids, want_logits)
+    def head(h, lm_head, ids=None, want_logits=True, pred=None):
+        lg, pred, res = inner_head(h, lm_head, ids, want_logits, pred=pred)
         calls.append(("head", np16(h), None if ids is None else ids.reshape(-1).tolist(), pred.cpu().tolist(),
                       res.cpu().tolist()))
         return lg, pred, res
 
-    def ffn_norm(hn, lw, layer_idx, input_ids, h, weight, residual=None):
+    def ffn_norm(hn, lw, layer_idx, input_ids, h, weight, residual=None, ids_owned=False):
         # the layer's FFN output from the same launch without its tail (the tail
         # variant's own output is the same, bit for bit), then the fused launch
         out, _ = ffn(hn, lw, layer_idx, input_ids)
-        fused = inner_ffn_norm(hn, lw, layer_idx, input_ids, h, weight, residual)
+        fused = inner_ffn_norm(hn, lw, layer_idx, input_ids, h, weight, residual, ids_owned=ids_owned)
         assert fused is not None
         calls.append(("norm", np16(h), np16(out), None if residual is None else np16(residual.reshape(1, -1))[0],
                       np16(weight.reshape(1, -1))[0], np16(fused[0]), np16(fused[1])))
