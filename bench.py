@@ -65,7 +65,8 @@ def parse():
                          "the line")
     ap.add_argument("--configs", default="0,2,3,4", help="sub-workloads of --workload all")
     ap.add_argument("--stack-layers", type=int, default=43)
-    ap.add_argument("--stack-steps", type=int, default=16, help="decode steps of config 4 under --workload all")
+    ap.add_argument("--stack-steps", type=int, default=64,
+                    help="decode steps of config 4 under --workload all (the config's 64-step decode loop)")
     ap.add_argument("--layers", type=int, default=8, help="distinct layers rotated through (MALL defeat)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu-baseline", action="store_true")
