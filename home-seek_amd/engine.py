@@ -31,6 +31,8 @@ Divergences from the reference, all deliberate:
 """
 from __future__ import annotations
 
+import warnings
+
 import torch
 
 from . import ops
@@ -163,6 +165,10 @@ class HomeSeekMoEEngine:
                                             self.store.shared_entry(layer_idx), out_f32=out_f32)
         return out.reshape(B, T, D).to(hidden_states.dtype), set()
 
+    # the persistent one-launch layer kernel (False: the router and the staged
+    # expert kernels, which give the same values and need no co-resident grid)
+    use_one_launch_layer = True
+
     def _one_launch_layer(self, flat: torch.Tensor, lw: dict, layer_idx: int, input_ids=None,
                           out_f32: torch.Tensor | None = None, out_bf16: torch.Tensor | None = None,
                           norm: ops.NormTail | None = None, ids_owned: bool = False) -> bool:
@@ -175,7 +181,7 @@ class HomeSeekMoEEngine:
         may still refer to them (no private copy is made).  -> False (and
         nothing launched) when it does not apply."""
         gate_w = lw.get("ffn.gate.weight")
-        if gate_w is None:
+        if gate_w is None or not self.use_one_launch_layer:
             return False
         tid2eid = lw.get("ffn.gate.tid2eid")
         m = flat.shape[0]
@@ -239,6 +245,10 @@ class HomeSeekMoEEngine:
             h2 = rms_norm(h2, self.norm_weight, self.config.rms_norm_eps)
         return h2
 
+    # a verify whose layer kernel reports a give-up runs again on the staged
+    # kernels (False: it raises HsmoeError instead)
+    verify_fallback = True
+
     @torch.no_grad()
     def _mtp_verify_batched(self, draft_ids, temperature: float = 0.6, main_pred_id=None):
         """One fused forward of [main_pred, drafts] (engine.py:2431-2540) ->
@@ -260,9 +270,30 @@ class HomeSeekMoEEngine:
             words = [w.to(torch.int64) for w in ops.moe_layer_status_words(self.device)]
             vals = torch.cat([result] + words).tolist()
             if any(vals[2:]):
-                ops.clear_moe_layer_status(self.device)  # reported once; later verifies start clean
-                raise ops._lib.HsmoeError(f"moe_layer_kernel: a cross-workgroup wait gave up (status "
-                                          f"{max(vals[2:])}); this verify's outputs are not valid")
+                # a cross-workgroup wait of the persistent layer kernel gave up
+                # (its grid was not co-resident, e.g. beside another kernel):
+                # reported once, then the verify runs again on the router and
+                # staged expert kernels, which need no co-residency and give
+                # the same values
+                ops.clear_moe_layer_status(self.device)
+                if not self.verify_fallback:
+                    raise ops._lib.HsmoeError(f"moe_layer_kernel: a cross-workgroup wait gave up (status "
+                                              f"{max(vals[2:])}); this verify's outputs are not valid")
+                warnings.warn(f"moe_layer_kernel: a cross-workgroup wait gave up (status {max(vals[2:])}); "
+                              f"the verify runs again on the staged kernels", RuntimeWarning, stacklevel=2)
+                self._restore_verify_state(snap, 0, t_total)
+                snap = self._snapshot_verify_state()
+                had = self.__dict__.get("use_one_launch_layer")
+                self.use_one_launch_layer = False
+                try:
+                    _, hf = self._forward_stack(combined)
+                finally:
+                    if had is None:
+                        del self.use_one_launch_layer
+                    else:
+                        self.use_one_launch_layer = had
+                logits, pred, result = ops.lm_head_accept(hf, self.lm_head, combined.reshape(-1))
+                vals = result.tolist()
             n_accept, bonus_row = vals[0], vals[1]
             bonus_logits = logits[bonus_row:bonus_row + 1]
         finally:

@@ -243,9 +243,9 @@ def test_verify_reads_status_and_accepts(model):
 
 def test_status_word_raises_once_and_restores_position(model):
     """A nonzero sticky status word (written from the host: no kernel gives up
-    here) makes _mtp_verify_batched and GreedyDecoder.result() raise
-    HsmoeError, restores _global_pos, and is cleared by the report, so the
-    next verify runs clean."""
+    here) makes _mtp_verify_batched (with verify_fallback off) and
+    GreedyDecoder.result() raise HsmoeError, restores _global_pos, and is
+    cleared by the report, so the next verify runs clean."""
     from home_seek_amd._lib import HsmoeError
     from home_seek_amd.engine import GreedyDecoder
     eng, so = model
@@ -258,8 +258,12 @@ def test_status_word_raises_once_and_restores_position(model):
     assert words and all(int(w.item()) == 0 for w in words)
     pos = eng._global_pos
     words[0].fill_(1 + 4609)
-    with pytest.raises(HsmoeError):
-        eng._mtp_verify_batched(drafts, 0.0, main_pred_id=main)
+    eng.verify_fallback = False
+    try:
+        with pytest.raises(HsmoeError):
+            eng._mtp_verify_batched(drafts, 0.0, main_pred_id=main)
+    finally:
+        del eng.verify_fallback
     assert eng._global_pos == pos
     assert ops.moe_layer_status(dev) == 0
     assert eng._mtp_verify_batched(drafts, 0.0, main_pred_id=main)[0] == 1
@@ -351,22 +355,33 @@ def test_checkpoint_round_trip_through_the_loader(model, tmp_path):
 
 def test_layer_status_word_fails_the_verify_and_the_decoder(model):
     """A nonzero sticky status word in a layer workspace (written here from the
-    host: no kernel gives up) makes _mtp_verify_batched and
-    GreedyDecoder.result() raise, leaves _global_pos where it was, and is
-    reported once (cleared after the raise)."""
+    host: no kernel gives up) makes _mtp_verify_batched run again on the
+    staged kernels (a warning; the values of a clean verify), or raise with
+    verify_fallback off, leaving _global_pos where it was; makes
+    GreedyDecoder.result() raise; and is reported once (cleared)."""
     from home_seek_amd import _lib
     from home_seek_amd.engine import GreedyDecoder
     eng, _ = model
     dev = eng.device
     main = torch.tensor([[7]], dtype=torch.int64, device=dev)
     drafts = torch.tensor([[5, 6]], dtype=torch.int64, device=dev)
-    eng._mtp_verify_batched(drafts, main_pred_id=main)  # the layer workspaces exist after this
+    n0, lg0 = eng._mtp_verify_batched(drafts, main_pred_id=main)  # the layer workspaces exist after this
     words = ops.moe_layer_status_words(dev)
     assert words and ops.moe_layer_status(dev) == 0
     pos = eng._global_pos
     words[0].fill_(1 + 4612)
-    with pytest.raises(_lib.HsmoeError, match="gave up"):
-        eng._mtp_verify_batched(drafts, main_pred_id=main)
+    with pytest.warns(RuntimeWarning, match="gave up"):
+        n1, lg1 = eng._mtp_verify_batched(drafts, main_pred_id=main)
+    assert n1 == n0 and torch.equal(lg1, lg0) and eng._global_pos == pos + n0
+    assert ops.moe_layer_status(dev) == 0 and eng.use_one_launch_layer
+    eng._global_pos = pos
+    eng.verify_fallback = False
+    try:
+        words[0].fill_(1 + 4612)
+        with pytest.raises(_lib.HsmoeError, match="gave up"):
+            eng._mtp_verify_batched(drafts, main_pred_id=main)
+    finally:
+        del eng.verify_fallback
     assert eng._global_pos == pos
     assert ops.moe_layer_status(dev) == 0
     n, logits = eng._mtp_verify_batched(drafts, main_pred_id=main)  # a clean verify works again
