@@ -6,10 +6,13 @@
 //   pred[t]; the bonus row is the first mismatch (or the last row).
 // Each logit is the correctly rounded bf16 of the exact dot product (bf16 x
 // bf16 products are exact in fp64, and so are the sums met in practice), in
-// one of two forms:
+// one of three forms:
+//  - 1 token, d <= 4096: one wave per vocab row, 1 KB per load instruction,
+//    the lane's hidden-state columns in fp64 registers, the row's partial
+//    sums added across the wave (lm_head_row_kernel);
 //  - 2..4 tokens: v_mfma_f64_4x4x4_4b_f64 over 4-row tiles, the bf16 hidden
 //    states in LDS (lm_head_mfma_kernel);
-//  - 1 or 5..8 tokens: one lane per vocab row summing in fp64 FMAs, the
+//  - 1 token with d > 4096, or 5..8 tokens: one lane per vocab row summing in fp64 FMAs, the
 //    hidden states widened to fp64 on their way into LDS when they fit
 //    (n_tok * d * 8 <= kLdsHBytes), else widened into the workspace by
 //    widen_h_kernel and read from there (lm_head_kernel); the inner loop reads
@@ -72,6 +75,102 @@ __device__ void accept_tail(const int64_t* __restrict__ ids, int64_t* __restrict
   result_out[0] = n_acc;
   result_out[1] = n_acc;
   __hip_atomic_store(&ws->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------- one token, row per wave
+// One token, d = 512 kC <= 4096: a wave takes whole vocab rows, each load
+// instruction reading 1 KB of one row (lane l: the 16-byte chunks l, l + 64,
+// ...), the form HBM streams fastest (measured on a pure-load copy of the
+// 129,280 x 4096 head: 166 us, against 175 for 4 rows x 256 B and 202-216
+// for a row per lane).  The lane's columns of the hidden state are widened
+// to fp64 once, in registers; each row's partial sums (exact fp64 products,
+// summed in chunk then element order) are added across the wave by a
+// butterfly, so a logit is the row's exact sum rounded once to bf16 whenever
+// that sum is exact in fp64, as for the other forms.  Rows are dealt to
+// waves grid-stride; the next row's loads are issued before this row's
+// sums.
+constexpr int kRowWaves = 4;
+
+__device__ __forceinline__ double bf16_elem(const uint4& q, int e) {
+  const uint32_t word = e < 2 ? q.x : e < 4 ? q.y : e < 6 ? q.z : q.w;
+  return (double)__uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
+}
+
+template <int kC>
+__global__ void __launch_bounds__(64 * kRowWaves)
+    lm_head_row_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ hb, int64_t vocab,
+                       const int64_t* __restrict__ ids, uint16_t* __restrict__ logits, int64_t* __restrict__ pred_out,
+                       int64_t* __restrict__ result_out, Workspace* __restrict__ ws) {
+  __shared__ unsigned long long s_key[kRowWaves];
+  __shared__ int s_last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int kRowQ = 64 * kC;  // 16-byte chunks per row
+  double hv[kC][8];
+#pragma unroll
+  for (int j = 0; j < kC; ++j) {
+    const uint4 q = reinterpret_cast<const uint4*>(hb)[lane + 64 * j];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) hv[j][e] = bf16_elem(q, e);
+  }
+  const uint4* __restrict__ wq = reinterpret_cast<const uint4*>(w) + lane;
+  const int64_t nwv = (int64_t)gridDim.x * kRowWaves;
+  unsigned long long key = 0;
+  auto load = [&](uint4 (&q)[kC], int64_t v) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < kC; ++j) q[j] = wq[v * kRowQ + 64 * j];
+  };
+  auto sum_row = [&](const uint4 (&q)[kC], int64_t v) __attribute__((always_inline)) {
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 0; j < kC; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = __fma_rn(hv[j][e], bf16_elem(q[j], e), acc);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    const uint32_t bits = f64_to_bf16_bits(acc);
+    if (lane == 0 && logits) logits[v] = (uint16_t)bits;
+    const unsigned long long k1 = logit_key(bits, v);
+    key = k1 > key ? k1 : key;
+  };
+  int64_t v = (int64_t)blockIdx.x * kRowWaves + wave;
+  uint4 qa[kC], qb[kC];
+  if (v < vocab) load(qa, v);
+  // two rows per turn: the row after next is loaded while this one is summed
+  while (v < vocab) {
+    const int64_t v1 = v + nwv;
+    if (v1 < vocab) load(qb, v1);
+    sum_row(qa, v);
+    if (v1 >= vocab) break;
+    const int64_t v2 = v1 + nwv;
+    if (v2 < vocab) load(qa, v2);
+    sum_row(qb, v1);
+    v = v2;
+  }
+  if (lane == 0) s_key[wave] = key;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long k = 0;
+#pragma unroll
+    for (int q2 = 0; q2 < kRowWaves; ++q2) k = s_key[q2] > k ? s_key[q2] : k;
+    __hip_atomic_fetch_max(&ws->key[0], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(&ws->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+  __syncthreads();
+  if (s_last && threadIdx.x == 0) accept_tail<1>(ids, pred_out, result_out, ws);
+}
+
+template <int kC>
+int launch_row(const uint16_t* w, const uint16_t* h, int64_t vocab, const int64_t* ids, uint16_t* logits,
+               int64_t* pred, int64_t* result, Workspace* ws, hipStream_t st) {
+  constexpr int64_t kBlocks = 512;  // two workgroups of 4 waves per CU
+  const int64_t need = (vocab + kRowWaves - 1) / kRowWaves;
+  const unsigned nb = (unsigned)(need < kBlocks ? need : kBlocks);
+  hipLaunchKernelGGL((lm_head_row_kernel<kC>), dim3(nb), dim3(64 * kRowWaves), 0, st, w, h, vocab, ids, logits, pred,
+                     result, ws);
+  return check_launch("hsmoe_lm_head_accept");
 }
 
 // ------------------------------------------------------------- fp64 MFMA form
@@ -389,6 +488,19 @@ extern "C" int hsmoe_lm_head_accept(const void* h, const void* lm_head, int64_t 
       case 2: return launch_mfma<2>(w, hb, d, vocab, ids, lg, pred_out, result_out, ws, st);
       case 3: return launch_mfma<3>(w, hb, d, vocab, ids, lg, pred_out, result_out, ws, st);
       default: return launch_mfma<4>(w, hb, d, vocab, ids, lg, pred_out, result_out, ws, st);
+    }
+  }
+  if (n_tok == 1 && d <= 4096 && aligned(h, 16)) {  // one token: row per wave (d > 4096: row per lane)
+    const uint16_t* hb = (const uint16_t*)h;
+    switch (d / 512) {
+      case 1: return launch_row<1>(w, hb, vocab, ids, lg, pred_out, result_out, ws, st);
+      case 2: return launch_row<2>(w, hb, vocab, ids, lg, pred_out, result_out, ws, st);
+      case 3: return launch_row<3>(w, hb, vocab, ids, lg, pred_out, result_out, ws, st);
+      case 4: return launch_row<4>(w, hb, vocab, ids, lg, pred_out, result_out, ws, st);
+      case 5: return launch_row<5>(w, hb, vocab, ids, lg, pred_out, result_out, ws, st);
+      case 6: return launch_row<6>(w, hb, vocab, ids, lg, pred_out, result_out, ws, st);
+      case 7: return launch_row<7>(w, hb, vocab, ids, lg, pred_out, result_out, ws, st);
+      default: return launch_row<8>(w, hb, vocab, ids, lg, pred_out, result_out, ws, st);
     }
   }
   double* h64 = (double*)((char*)workspace + h64_offset());

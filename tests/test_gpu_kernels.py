@@ -106,7 +106,9 @@ def test_router_ties_and_no_bias(dev):
      # six tokens of 4096: fp64 hidden states past the LDS budget, widened into the workspace by a launch of their own
      (6, 3001, 4096),
      # the largest hidden size the entry point takes: 64 KiB of bf16 hidden states in the MFMA form's LDS
-     (2, 3001, 8192), (3, 1001, 8192), (4, 2049, 8192), (1, 1001, 8192)])
+     (2, 3001, 8192), (3, 1001, 8192), (4, 2049, 8192), (1, 1001, 8192),
+     # one token, row per wave: the full head, a hidden size of 3 chunks per lane, fewer rows than waves
+     (1, 129280, 4096), (1, 33333, 1536), (1, 5, 2048)])
 def test_lm_head_logits_argmax_bit_exact(dev, n_tok, vocab, d):
     seed = 7 + n_tok
     lm = synthetic.normal_bf16(seed, synthetic.tag(synthetic.KIND_LM_HEAD), (vocab, d), 0.0, 0.02, dev)
