@@ -141,8 +141,8 @@ def roofline(kernel: str, nbytes: int, us: float, traffic=None, **extra) -> dict
 
 def read_ceiling(torch, buf, stream) -> dict:
     """The HBM read rate a single pass over resident weights reaches on this
-    device: hsmoe_xor_checksum (a read-only stream, 16 loads of 16 bytes in
-    flight per lane) over distinct 1 GiB slices of `buf` in rotation, far
+    device: hsmoe_xor_checksum (a read-only stream, 8 loads of 16 bytes in
+    flight per lane, one workgroup per CU) over distinct 1 GiB slices of `buf` in rotation, far
     beyond the 256 MB Infinity Cache; median of the per-replay rates."""
     from home_seek_amd import ops
     gib = 1 << 30

@@ -8,12 +8,16 @@
 // The same kernel is the library's measure of the read bandwidth a
 // single-pass stream reaches on the device (it moves nothing but loads).
 //
-// Pass 1: workgroup b XORs the 64 KiB chunks b, b + G, b + 2G, ...: every
-// lane has 16 loads of 16 bytes in flight per chunk (the chunk's next 4 KiB
+// Pass 1: workgroup b XORs the 32 KiB chunks b, b + G, b + 2G, ...: every
+// lane has 8 loads of 16 bytes in flight per chunk (the chunk's next 4 KiB
 // per load instruction of the workgroup, 1 KiB contiguous per wave), and
 // the lane's words of the next chunk are loaded before the current chunk is
-// folded.  The workgroup's XOR goes to partial[b].  Pass 2: one workgroup
-// folds the G partials.
+// folded.  G is one workgroup per CU: about 32-64 KiB in flight per CU is
+// where the stream reads fastest on MI355X (6.45-6.49 TB/s over 1 GiB);
+// 4 workgroups of 64 KiB chunks per CU (256 KiB in flight) read at
+// 5.87-5.92 TB/s, the queues behind each channel only adding latency.
+// The workgroup's XOR goes to partial[b].  Pass 2: one workgroup folds the
+// G partials.
 #include "hsmoe_internal.h"
 #include "hsmoe_common.h"
 
@@ -21,8 +25,8 @@ namespace hsmoe {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kLoads = 16;                                // 16-byte loads per lane per chunk
-constexpr int64_t kChunk = (int64_t)kThreads * kLoads;  // 16-byte words per chunk (64 KiB)
+constexpr int kLoads = 8;                                 // 16-byte loads per lane per chunk
+constexpr int64_t kChunk = (int64_t)kThreads * kLoads;  // 16-byte words per chunk (32 KiB)
 constexpr int kMaxGrid = 4096;
 
 __device__ __forceinline__ uint4 xor4(uint4 a, uint4 b) {
@@ -93,7 +97,7 @@ int grid_for(int64_t n16) {
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
   const int64_t n_chunks = (n16 + kChunk - 1) / kChunk;
-  int64_t g = 4 * (int64_t)cus;  // 4 workgroups (16 waves) per CU
+  int64_t g = cus;  // one workgroup (4 waves) per CU
   if (g > kMaxGrid) g = kMaxGrid;
   if (g > n_chunks) g = n_chunks;
   return g < 1 ? 1 : (int)g;
