@@ -189,7 +189,10 @@ int launch_row(const uint16_t* w, const uint16_t* h, int64_t vocab, const int64_
 // 1 KB over 4 rows at 4.8.  Tiles are dealt to waves grid-stride (wave w
 // takes tiles w, w + waves, ...), so that the grid reads one contiguous
 // window of the head at a time (a contiguous run of tiles per wave was ~4%
-// slower), with the load pipeline running on across a wave's tiles.
+// slower), with the load pipeline running on across a wave's tiles: the
+// next group's loads go out while a group is multiplied (one group ahead:
+// 202 us at T = 3 over the 129,280 x 4096 head against 207 with four; the
+// same loads with no arithmetic run at 182-187).
 // The hidden states sit in LDS as bf16 [4][d]; a B lane reads the same
 // columns as its A lane in 16-byte LDS loads.  Products of bf16 values are
 // exact in fp64 and every partial sum is a subset sum of a row's products,
@@ -197,7 +200,7 @@ int launch_row(const uint16_t* w, const uint16_t* h, int64_t vocab, const int64_
 // exact in fp64, as for the row-per-lane form.
 constexpr int kMfmaWaves = 4;
 constexpr int kMfmaW = 4;                  // 16-byte loads per lane and group (8 k each)
-constexpr int kMfmaAhead = 16 / kMfmaW;    // groups in flight per wave (256 bytes per lane)
+constexpr int kMfmaAhead = 1;             // groups in flight per wave (64 bytes per lane)
 constexpr int kMfmaGroupCols = 128 * kMfmaW;  // columns of a row per group
 constexpr int kMfmaResidentWaves = 4096;   // 256 CUs x 4 SIMDs x 4 waves
 
