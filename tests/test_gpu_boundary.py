@@ -117,7 +117,7 @@ def test_stable_topk_by_name(dev):
     assert router.stable_topk(s, 3).cpu().tolist() == [[1, 2, 4]]
 
 
-@pytest.mark.parametrize("nbytes", [0, 16, 48, (64 << 10) + 48, (3 << 20) + 16, 100 << 20])
+@pytest.mark.parametrize("nbytes", [0, 16, 48, (64 << 10) + 48, (3 << 20) + 16, (256 << 15) + 16, 100 << 20])
 def test_xor_checksum_matches_host(dev, nbytes):
     g = torch.Generator(device="cpu").manual_seed(nbytes % 1000)
     host = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, generator=g)

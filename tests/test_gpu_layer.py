@@ -213,10 +213,10 @@ def test_workspace_rearms_before_the_tags_wrap(layer, dev):
     assert ops.moe_layer_status(dev) == 0
 
 
-def routed(x, idx, table, shared, w=None, weight_all=1.0, token_ids=None, k=K):
+def routed(x, idx, table, shared, w=None, weight_all=1.0, token_ids=None, k=K, kind=ops.SCALE_E8M0):
     f32 = torch.empty(x.shape[0], D, dtype=torch.float32, device=x.device)
     bf = torch.empty(x.shape[0], D, dtype=torch.bfloat16, device=x.device)
-    out, _ = ops.moe_layer_decode_routed(x, idx, table, ops.SCALE_E8M0, shared, I, topk_w=w, weight_all=weight_all,
+    out, _ = ops.moe_layer_decode_routed(x, idx, table, kind, shared, I, topk_w=w, weight_all=weight_all,
                                          token_ids=token_ids, top_k=k, out_f32=f32, out_bf16=bf)
     return out, f32
 
@@ -285,3 +285,36 @@ def test_routed_layer_one_slot_alone(layer, dev, ids):
     torch.cuda.synchronize()
     assert ops.moe_layer_status(dev) == 0
     assert torch.equal(a[1], f32) and torch.equal(a[0], b16)
+
+
+@pytest.mark.parametrize("fmt", ["e8m0", "fp32", "bf16"])
+def test_lone_slot_every_format(layer, dev, fmt):
+    """One token, one routed slot and no shared expert (the down items write
+    the rows themselves) in each routed weight format -- FP4 with E8M0 scales
+    and with fp32 scales (the two gate/up run paths) and dequantised bf16 (the
+    per-item path): bit-identical to moe_decode; an invalid id gives the zero
+    output."""
+    store, _, _ = layer
+    eid = 77
+    w1, s1, w3, s3, w2, s2 = store.expert_views(0, eid)
+    if fmt == "e8m0":
+        table, kind = store.table(0), ops.SCALE_E8M0
+    else:
+        if fmt == "bf16":
+            ent = (ops.fp4_dequant_bf16(w1, s1), ops.fp4_dequant_bf16(w3, s3), ops.fp4_dequant_bf16(w2, s2))
+        else:
+            ent = (w1, s1.to(torch.float32), w3, s3.to(torch.float32), w2, s2.to(torch.float32))
+        table, kind = ops.expert_table([ent if e == eid else None for e in range(E)], dev), ops.SCALE_F32
+    x = synthetic.hidden(SEED, 970, 1, D, dev)
+    idx = torch.tensor([[eid]], dtype=torch.int64, device=dev)
+    w = torch.tensor([[0.75]], dtype=torch.float32, device=dev)
+    a = routed(x, idx, table, None, w=w, k=1, kind=kind)
+    f32 = torch.empty(1, D, dtype=torch.float32, device=dev)
+    b16, _ = ops.moe_decode(x, idx, w, table, kind, None, 10.0, out_f32=f32, d=D, i=I)
+    torch.cuda.synchronize()
+    assert ops.moe_layer_status(dev) == 0
+    assert torch.equal(a[1], f32) and torch.equal(a[0], b16)
+    z = routed(x, torch.tensor([[-1]], dtype=torch.int64, device=dev), table, None, w=w, k=1, kind=kind)
+    torch.cuda.synchronize()
+    assert ops.moe_layer_status(dev) == 0
+    assert torch.count_nonzero(z[1]) == 0 and torch.count_nonzero(z[0]) == 0
