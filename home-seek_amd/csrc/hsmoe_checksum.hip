@@ -93,11 +93,8 @@ __global__ void __launch_bounds__(kThreads) xor_fold_kernel(const uint4* __restr
 }
 
 int grid_for(int64_t n16) {
-  int cus = 256, dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 256;
   const int64_t n_chunks = (n16 + kChunk - 1) / kChunk;
-  int64_t g = cus;  // one workgroup (4 waves) per CU
+  int64_t g = device_cus();  // one workgroup (4 waves) per CU
   if (g > kMaxGrid) g = kMaxGrid;
   if (g > n_chunks) g = n_chunks;
   return g < 1 ? 1 : (int)g;

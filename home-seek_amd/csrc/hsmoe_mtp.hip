@@ -165,9 +165,12 @@ __global__ void __launch_bounds__(64 * kRowWaves)
 template <int kC>
 int launch_row(const uint16_t* w, const uint16_t* h, int64_t vocab, const int64_t* ids, uint16_t* logits,
                int64_t* pred, int64_t* result, Workspace* ws, hipStream_t st) {
-  constexpr int64_t kBlocks = 512;  // two workgroups of 4 waves per CU
+  // one workgroup of 4 waves per CU: 168-174 us over the 129,280 x 4096 head
+  // against 179-180 with two per CU (320 or 384 workgroups, uneven over the
+  // CUs: 185-205)
+  const int64_t blocks = device_cus();
   const int64_t need = (vocab + kRowWaves - 1) / kRowWaves;
-  const unsigned nb = (unsigned)(need < kBlocks ? need : kBlocks);
+  const unsigned nb = (unsigned)(need < blocks ? need : blocks);
   hipLaunchKernelGGL((lm_head_row_kernel<kC>), dim3(nb), dim3(64 * kRowWaves), 0, st, w, h, vocab, ids, logits, pred,
                      result, ws);
   return check_launch("hsmoe_lm_head_accept");
