@@ -142,21 +142,34 @@ def roofline(kernel: str, nbytes: int, us: float, traffic=None, **extra) -> dict
 def read_ceiling(torch, buf, stream) -> dict:
     """The HBM read rate a single pass over resident weights reaches on this
     device: hsmoe_xor_checksum (a read-only stream, 8 loads of 16 bytes in
-    flight per lane, one workgroup per CU) over distinct 1 GiB slices of `buf` in rotation, far
-    beyond the 256 MB Infinity Cache; median of the per-replay rates."""
+    flight per lane, one workgroup per CU) over distinct slices of `buf` in
+    rotation, far beyond the 256 MB Infinity Cache.  The median time per call
+    over 1 GiB slices and over 2 GiB slices is fitted as t = a + bytes / rate,
+    so that the rate leaves out a call's fixed cost (its one-workgroup fold
+    launch and the gap before it, ~3% of a 1 GiB call)."""
     from home_seek_amd import ops
     gib = 1 << 30
-    n = min(8, buf.numel() // gib)
-    if n < 2:
+
+    def per_call(size):
+        n = min(8, buf.numel() // size)
+        if n < 1:
+            return None, 0
+        slices = [buf[j * size:(j + 1) * size] for j in range(n)]
+        outs = [torch.empty(16, dtype=torch.uint8, device=buf.device) for _ in range(n)]
+        _, samples = timed_launches(torch, stream, lambda j: ops.xor_checksum(slices[j], outs[j]), n, max(4 * n, 8), n)
+        return statistics.median(samples), n
+
+    t1, n1 = per_call(gib)
+    t2, n2 = per_call(2 * gib)
+    if t1 is None or t2 is None or t2 <= t1:
         return None
-    slices = [buf[j * gib:(j + 1) * gib] for j in range(n)]
-    outs = [torch.empty(16, dtype=torch.uint8, device=buf.device) for _ in range(n)]
-    _, samples = timed_launches(torch, stream, lambda j: ops.xor_checksum(slices[j], outs[j]), n, 4 * n, n)
-    us = statistics.median(samples)
-    return {"gbs": round(gib / (us * 1e-6) / 1e9, 1), "bytes_per_launch": gib, "us_per_launch": round(us, 2),
-            "slices": n, "frac_of_hbm_peak": round(gib / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "method": "hsmoe_xor_checksum over distinct 1 GiB slices of the expert store, rotated in a HIP graph "
-                      "(the stream launch + a one-workgroup fold); median of per-replay times"}
+    gbs = gib / ((t2 - t1) * 1e-6) / 1e9
+    return {"gbs": round(gbs, 1), "us_per_gib": round(t2 - t1, 2), "call_overhead_us": round(2 * t1 - t2, 2),
+            "us_per_call_1gib": round(t1, 2), "us_per_call_2gib": round(t2, 2), "slices": [n1, n2],
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "method": "hsmoe_xor_checksum over distinct 1 GiB and 2 GiB slices of the store, each size rotated in a HIP "
+                      "graph; median time per call fitted as t = a + bytes / rate (a: the fold launch and the gap "
+                      "before it)"}
 
 
 def with_ceiling(roof: dict | None, ceiling: dict | None) -> dict | None:
