@@ -119,17 +119,32 @@ __device__ __forceinline__ int block_sum(int v, int* s_red) {
 __global__ void __launch_bounds__(kThreads) prefill_group_kernel(PrefillParams p) {
   __shared__ int s_e[kMaxPairs];
   __shared__ int s_cnt[kMaxExperts];
+  __shared__ bool s_ok[kMaxExperts];  // expert e has a table entry
   __shared__ int s_red[kThreads / 64];
   __shared__ int s_wc[kThreads / 64];
   const int E = p.n_experts, K = p.top_k, P = p.m * K, me = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int e = threadIdx.x; e < E; e += kThreads) s_cnt[e] = 0;
+  // which experts have a table entry: one load per expert, not one per pair
+  for (int e = threadIdx.x; e < E; e += kThreads) {
+    s_cnt[e] = 0;
+    s_ok[e] = p.table[(int64_t)e * 6] != 0;
+  }
   __syncthreads();
-  for (int q = threadIdx.x; q < P; q += kThreads) {
-    const int64_t e = p.idx[q];
-    const bool ok = e >= 0 && e < E && p.table[e * 6] != 0;
-    s_e[q] = ok ? (int)e : -1;
-    if (ok) atomicAdd(&s_cnt[e], 1);
+  // the pair ids, kIdBatch loads of a thread in flight at once
+  constexpr int kIdBatch = 8;
+  for (int q0 = threadIdx.x; q0 < P; q0 += kIdBatch * kThreads) {
+    int64_t ev[kIdBatch];
+#pragma unroll
+    for (int j = 0; j < kIdBatch; ++j) ev[j] = q0 + j * kThreads < P ? p.idx[q0 + j * kThreads] : -1;
+#pragma unroll
+    for (int j = 0; j < kIdBatch; ++j) {
+      const int q = q0 + j * kThreads;
+      if (q >= P) break;
+      const int64_t e = ev[j];
+      const bool ok = e >= 0 && e < E && s_ok[e];
+      s_e[q] = ok ? (int)e : -1;
+      if (ok) atomicAdd(&s_cnt[e], 1);
+    }
   }
   __syncthreads();
   if (me == E) {
