@@ -91,10 +91,24 @@ __global__ void __launch_bounds__(kThreads)
                      int64_t d, float eps, uint4* __restrict__ h_out, uint4* __restrict__ out) {
   __shared__ float part[3][kThreads / 64];
   const int chunks = (int)(d / 8), tid = (int)threadIdx.x;
+  // the norm weights and the residual depend on nothing: their loads go out
+  // with the token id's, not after the barriers that the sums need
+  const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
+  uint4 env[4], hnv[4], rsv[4], wv[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int c = tid + kThreads * b;
+    env[b] = hnv[b] = rsv[b] = wv[b] = zero;
+    if (c < chunks) {
+      env[b] = enorm[c];
+      hnv[b] = hnorm[c];
+      if (res) rsv[b] = res[c];
+      wv[b] = w[c];
+    }
+  }
   const int64_t id = tok[0];
   const bool have = id >= 0 && id < vocab;
   const uint4* er = embed + (have ? id : 0) * chunks;
-  const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
   uint4 ev[4], gv[4];
   float se = 0.0f, sg = 0.0f;
 #pragma unroll
@@ -121,9 +135,9 @@ __global__ void __launch_bounds__(kThreads)
   for (int b = 0; b < 4; ++b) {
     const int c = tid + kThreads * b;
     if (c < chunks) {
-      const uint4 e = norm_scale_chunk(ev[b], enorm[c], ie);
-      uint4 h = norm_add_chunk(norm_scale_chunk(gv[b], hnorm[c], ig), e);
-      if (res) h = norm_add_chunk(h, res[c]);
+      const uint4 e = norm_scale_chunk(ev[b], env[b], ie);
+      uint4 h = norm_add_chunk(norm_scale_chunk(gv[b], hnv[b], ig), e);
+      if (res) h = norm_add_chunk(h, rsv[b]);
       ev[b] = h;
       h_out[c] = h;
       sh = norm_sumsq_chunk(h, sh);
@@ -136,7 +150,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const int c = tid + kThreads * b;
-    if (c < chunks) out[c] = norm_scale_chunk(ev[b], w[c], ih);
+    if (c < chunks) out[c] = norm_scale_chunk(ev[b], wv[b], ih);
   }
 }
 
